@@ -1,0 +1,96 @@
+/* sgl/qlinear.h — device-resident quantized linear layer (MI355X / gfx950).
+ *
+ * New entry points with no one-to-one counterpart in the reference: the reference dequantizes
+ * AWQ/GPTQ/Marlin/CT/MXFP4 weights to f32 at load time (reference src/safetensors.c:271-471,
+ * src/qweight.c) and multiplies the f32 copy with sgl_matmul_nt (reference src/ops.c:243-279),
+ * or multiplies int8 weights with sgl_matmul_w8a16 (reference src/quant.c:44-89).  A
+ * sgl_qlinear keeps the packed weight resident in HBM instead and runs the multiply on it:
+ *
+ *   load:     sgl_qlinear_create*  takes the same buffers (and the same validation, error
+ *             returns and log lines) as the matching sgl_qweight_dequant* call, so the loader's
+ *             quant_get (reference src/safetensors.c:348-457) can pass them through unchanged.
+ *   forward:  sgl_qlinear_forward  computes C[M,N] = A[M,K] W^T + bias, where W is exactly the
+ *             matrix sgl_qweight_dequant* would have produced; replaces the proj_nt dispatch
+ *             (reference src/llama.c:876-884).
+ *   checking: sgl_qlinear_dequant  writes that W (f32 [N,K]) to device memory, bit-identical
+ *             to the reference dequant.
+ *   MoE:      sgl_qmoe_forward     routed expert FFN with the weighted combine of reference
+ *             src/deepseek.c:655-677 (routing itself is an input).
+ *
+ * All pointers passed to create* are host pointers.  Pointers passed to forward/dequant/moe are
+ * device pointers; `stream` is a hipStream_t (NULL = default stream).  A handle is bound to
+ * the device it was created on and must not be used by two threads at once.  Functions return
+ * 0 (or a handle) on success and -1 (or NULL) after logging the reason.
+ */
+#ifndef SGL_QLINEAR_H
+#define SGL_QLINEAR_H
+
+#include <stdint.h>
+
+#include "sgl/qweight.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct sgl_qlinear sgl_qlinear;
+
+/* activation element types for forward / MoE */
+enum { SGL_QL_F32 = 0, SGL_QL_BF16 = 1, SGL_QL_F16 = 2 };
+
+/* AWQ (gemm / gemv) and GPTQ (incl. act-order g_idx, gptq_v2, 8-bit): same arguments as
+ * sgl_qweight_dequant.  A cfg with layout == SGL_QLAYOUT_MARLIN is routed to the Marlin
+ * decoder (g_idx must then be NULL, as in the reference). */
+sgl_qlinear *sgl_qlinear_create(const sgl_qcfg *cfg, const int32_t *qweight, int64_t qw_rows,
+                                int64_t qw_cols, const int32_t *qzeros, int64_t qz_rows,
+                                int64_t qz_cols, const float *scales, int64_t sc_rows,
+                                int64_t sc_cols, const int32_t *g_idx, int64_t g_n, int64_t N,
+                                int64_t K, int dev);
+/* Marlin layout: same arguments as sgl_qweight_dequant_marlin. */
+sgl_qlinear *sgl_qlinear_create_marlin(const sgl_qcfg *cfg, const int32_t *qweight,
+                                       int64_t qw_rows, int64_t qw_cols, const int32_t *qzeros,
+                                       int64_t qz_rows, int64_t qz_cols, const float *scales,
+                                       int64_t sc_rows, int64_t sc_cols, int64_t N, int64_t K,
+                                       int dev);
+/* compressed-tensors pack-quantized: same arguments as sgl_qweight_dequant_ct. */
+sgl_qlinear *sgl_qlinear_create_ct(const sgl_qcfg *cfg, const int32_t *wpacked, int64_t rows,
+                                   int64_t cols, const float *scales, int64_t sc_rows,
+                                   int64_t sc_cols, int64_t N, int64_t K, int dev);
+/* MXFP4: same arguments as sgl_qweight_dequant_mxfp4. */
+sgl_qlinear *sgl_qlinear_create_mxfp4(const uint8_t *wpacked, int64_t rows, int64_t cols,
+                                      const uint8_t *scales, int64_t sc_rows, int64_t sc_cols,
+                                      int64_t N, int64_t K, int dev);
+/* W8 per-row int8 (the operands of sgl_matmul_w8a16): W int8 [N,K], sw f32 [N]. */
+sgl_qlinear *sgl_qlinear_create_w8(const int8_t *W, const float *sw, int64_t N, int64_t K,
+                                   int dev);
+
+/* C[M,N] = A[M,K] * W^T + bias (bias may be NULL).  A is row-major with a_dtype elements,
+ * C is f32 row-major.  Any M >= 1. */
+int sgl_qlinear_forward(sgl_qlinear *ql, const void *A, int a_dtype, int64_t M,
+                        const float *bias, float *C, void *stream);
+
+/* W as f32 [N,K] into device memory: bit-identical to the reference dequant of the inputs. */
+int sgl_qlinear_dequant(sgl_qlinear *ql, float *out, void *stream);
+
+int64_t sgl_qlinear_out_features(const sgl_qlinear *ql);
+int64_t sgl_qlinear_in_features(const sgl_qlinear *ql);
+/* HBM bytes of the resident weight one forward streams (codes + scales + zeros). */
+int64_t sgl_qlinear_weight_bytes(const sgl_qlinear *ql);
+
+void sgl_qlinear_destroy(sgl_qlinear *ql);
+
+/* Routed-expert FFN of one MoE block (reference src/deepseek.c:655-677, fused gate/up):
+ * for each token t and slot j < k with e = topk_ids[t*k + j] >= 0:
+ *   gu = h_t * gate_up[e]^T ([2*mi]);  a_i = silu(gu_i) * gu_{mi+i};  o = a * down[e]^T ([E]);
+ *   out_t += topk_w[t*k + j] * o, slots summed in order j = 0..k-1 (deterministic).
+ * gate_up[e] is [2*mi, E], down[e] is [E, mi]; h is [T, E] (h_dtype), out f32 [T, E];
+ * topk_ids (int32) / topk_w (f32) are [T, k] device arrays. */
+int sgl_qmoe_forward(sgl_qlinear *const *gate_up, sgl_qlinear *const *down, int n_experts,
+                     const void *h, int h_dtype, int64_t T, const int32_t *topk_ids,
+                     const float *topk_w, int k, float *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SGL_QLINEAR_H */

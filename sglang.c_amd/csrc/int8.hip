@@ -1,0 +1,159 @@
+// int8.hip — per-row symmetric int8 quantization, int8 row dequant and the f32 NT matmul
+// behind the reference API entry points sgl_quant_rows_i8 / sgl_dequant_row_i8 /
+// sgl_matmul_nt (reference src/quant.c:13-42, src/ops.c:243-279), computed on the GPU.
+#include "sglq_dev.hpp"
+
+// One workgroup per row.  Arithmetic is the reference's, step for step, without contraction:
+// scale = maxabs / 127, inv = 1 / scale, v = trunc(x * inv +- 0.5) clamped to [-127, 127]
+// (reference src/quant.c:13-32); an all-zero row gives scale 0 and zero codes.
+__global__ __launch_bounds__(256) void k_quant_rows_i8(const float *__restrict__ x,
+                                                       int8_t *__restrict__ q,
+                                                       float *__restrict__ scales, int64_t dim) {
+#pragma clang fp contract(off)
+  const int64_t r = blockIdx.x;
+  const float *row = x + r * dim;
+  __shared__ float red[256];
+  float m = 0.f;
+  for (int64_t i = threadIdx.x; i < dim; i += 256) {
+    const float a = row[i] < 0 ? -row[i] : row[i];
+    if (a > m) m = a;
+  }
+  red[threadIdx.x] = m;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s && red[threadIdx.x + s] > red[threadIdx.x])
+      red[threadIdx.x] = red[threadIdx.x + s];
+    __syncthreads();
+  }
+  const float maxabs = red[0];
+  int8_t *qr = q + r * dim;
+  if (!(maxabs > 0)) {
+    for (int64_t i = threadIdx.x; i < dim; i += 256) qr[i] = 0;
+    if (threadIdx.x == 0) scales[r] = 0.f;
+    return;
+  }
+  const float scale = maxabs / 127.0f;
+  const float inv = 1.0f / scale;
+  for (int64_t i = threadIdx.x; i < dim; i += 256) {
+    const float xv = row[i];
+    const float p = xv * inv;
+    const float h = xv >= 0 ? 0.5f : -0.5f;
+    const float r = p + h;
+    // float -> int as the reference's x86 build converts (cvttss2si): out of range or NaN
+    // gives INT_MIN, e.g. a denormal row whose 1/scale overflows to inf
+    int v = (r >= -2147483648.0f && r < 2147483648.0f) ? (int)r : INT32_MIN;
+    v = v > 127 ? 127 : (v < -127 ? -127 : v);
+    qr[i] = (int8_t)v;
+  }
+  if (threadIdx.x == 0) scales[r] = scale;
+}
+
+__global__ void k_dequant_row_i8(const int8_t *__restrict__ q, float scale, float *__restrict__ o,
+                                 int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) o[i] = (float)q[i] * scale;
+}
+
+// f32 C[M,N] = A[M,K] W[N,K]^T + bias: one wave per (n, 8-row block), lanes stride K with fp32
+// fused multiply-add, combined across lanes in double.
+__global__ __launch_bounds__(256) void k_matmul_nt(const float *__restrict__ A,
+                                                   const float *__restrict__ W,
+                                                   const float *__restrict__ bias,
+                                                   float *__restrict__ C, int64_t M, int64_t N,
+                                                   int64_t K) {
+  const int64_t wid = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t mblocks = (M + 7) / 8;
+  if (wid >= N * mblocks) return;
+  const int64_t n = wid / mblocks, m0 = (wid % mblocks) * 8;
+  const float *wr = W + n * K;
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int64_t k = lane; k < K; k += 64) {
+    const float wv = wr[k];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      if (m0 + i < M) acc[i] = fmaf(A[(m0 + i) * K + k], wv, acc[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    double s = acc[i];
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if (lane == 0 && m0 + i < M) C[(m0 + i) * N + n] = (float)s + (bias ? bias[n] : 0.f);
+  }
+}
+
+extern "C" int sglq_quant_rows_i8_host(const float *x, int8_t *out, float *scales, int64_t rows,
+                                       int64_t dim) {
+  float *dx = nullptr, *ds = nullptr;
+  int8_t *dq = nullptr;
+  const size_t n = (size_t)(rows * dim);
+  if (rows <= 0 || dim <= 0) return 0;
+  SGLQ_HIP(hipMalloc(&dx, n * 4));
+  SGLQ_HIP(hipMalloc(&dq, n));
+  SGLQ_HIP(hipMalloc(&ds, (size_t)rows * 4));
+  SGLQ_HIP(hipMemcpy(dx, x, n * 4, hipMemcpyHostToDevice));
+  k_quant_rows_i8<<<(unsigned)rows, 256>>>(dx, dq, ds, dim);
+  SGLQ_HIP(hipGetLastError());
+  SGLQ_HIP(hipMemcpy(out, dq, n, hipMemcpyDeviceToHost));
+  SGLQ_HIP(hipMemcpy(scales, ds, (size_t)rows * 4, hipMemcpyDeviceToHost));
+  (void)hipFree(dx);
+  (void)hipFree(dq);
+  (void)hipFree(ds);
+  return 0;
+fail:
+  (void)hipFree(dx);
+  (void)hipFree(dq);
+  (void)hipFree(ds);
+  return -1;
+}
+
+extern "C" int sglq_dequant_row_i8_host(const int8_t *q, float scale, float *out, int64_t n) {
+  int8_t *dq = nullptr;
+  float *dout = nullptr;
+  if (n <= 0) return 0;
+  SGLQ_HIP(hipMalloc(&dq, (size_t)n));
+  SGLQ_HIP(hipMalloc(&dout, (size_t)n * 4));
+  SGLQ_HIP(hipMemcpy(dq, q, (size_t)n, hipMemcpyHostToDevice));
+  k_dequant_row_i8<<<sglq_blocks(n, 256), 256>>>(dq, scale, dout, n);
+  SGLQ_HIP(hipGetLastError());
+  SGLQ_HIP(hipMemcpy(out, dout, (size_t)n * 4, hipMemcpyDeviceToHost));
+  (void)hipFree(dq);
+  (void)hipFree(dout);
+  return 0;
+fail:
+  (void)hipFree(dq);
+  (void)hipFree(dout);
+  return -1;
+}
+
+extern "C" int sglq_matmul_nt_host(const float *A, const float *W, const float *bias, float *C,
+                                   int64_t M, int64_t N, int64_t K) {
+  float *dA = nullptr, *dW = nullptr, *dB = nullptr, *dC = nullptr;
+  if (M <= 0 || N <= 0) return 0;
+  SGLQ_HIP(hipMalloc(&dA, (size_t)(M * K) * 4));
+  SGLQ_HIP(hipMalloc(&dW, (size_t)(N * K) * 4));
+  SGLQ_HIP(hipMalloc(&dC, (size_t)(M * N) * 4));
+  SGLQ_HIP(hipMemcpy(dA, A, (size_t)(M * K) * 4, hipMemcpyHostToDevice));
+  SGLQ_HIP(hipMemcpy(dW, W, (size_t)(N * K) * 4, hipMemcpyHostToDevice));
+  if (bias) {
+    SGLQ_HIP(hipMalloc(&dB, (size_t)N * 4));
+    SGLQ_HIP(hipMemcpy(dB, bias, (size_t)N * 4, hipMemcpyHostToDevice));
+  }
+  {
+    const int64_t waves = N * ((M + 7) / 8);
+    k_matmul_nt<<<sglq_blocks(waves * 64, 256), 256>>>(dA, dW, dB, dC, M, N, K);
+  }
+  SGLQ_HIP(hipGetLastError());
+  SGLQ_HIP(hipMemcpy(C, dC, (size_t)(M * N) * 4, hipMemcpyDeviceToHost));
+  (void)hipFree(dA);
+  (void)hipFree(dW);
+  (void)hipFree(dB);
+  (void)hipFree(dC);
+  return 0;
+fail:
+  (void)hipFree(dA);
+  (void)hipFree(dW);
+  (void)hipFree(dB);
+  (void)hipFree(dC);
+  return -1;
+}

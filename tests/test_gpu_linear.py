@@ -1,0 +1,91 @@
+"""Forward parity on the GPU: sgl_qlinear_forward against the reference CPU path (the oracle's
+dequant + sgl_matmul_nt, or sgl_matmul_w8a16 for W8) on the same seeded inputs.
+Tolerance (BASELINE): max|y - y_ref| / max|y_ref| <= 1e-3."""
+import numpy as np
+import pytest
+
+import synth
+from linear_cases import build, oracle_forward, oracle_weight, product, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+FORMATS = ["gptq4", "gptq4_act", "gptq4_v2", "gptq4_noz", "gptq4_row", "gptq8", "awq4",
+           "awq4_gemv", "awq4_noz", "marlin4_asym", "marlin4_sym", "marlin8_asym", "marlin8_sym",
+           "ct4", "ct8", "mxfp4", "w8"]
+
+
+def _run(orc, fmt, N, K, Ms, dtypes=("f32", "bf16"), bias=False, seed=3):
+    import torch
+    kind, a = build(fmt, N, K, seed=seed)
+    ql = product(kind, a, N, K)
+    W = oracle_weight(orc, kind, a, N, K)
+    b = synth.normal(seed + 7, N, 0.1) if bias else None
+    for M in Ms:
+        A = synth.normal(seed + 100 + M, (M, K))
+        for dt in dtypes:
+            if dt == "bf16":
+                Ab = synth.bf16_bits_to_f32(synth.to_bf16_bits(A))
+                tA = torch.from_numpy(Ab).cuda().to(torch.bfloat16)
+            elif dt == "f16":
+                Ab = A.astype(np.float16).astype(np.float32)
+                tA = torch.from_numpy(Ab).cuda().to(torch.float16)
+            else:
+                Ab = A
+                tA = torch.from_numpy(A).cuda()
+            print(f"[gpu] forward {fmt} N={N} K={K} M={M} {dt}", flush=True)
+            tb = None if b is None else torch.from_numpy(b).cuda()
+            y = ql.forward(tA, bias=tb).cpu().numpy()
+            ref = oracle_forward(orc, kind, a, W, Ab, b)
+            e = rel_err(y, ref)
+            assert e <= TOL, (fmt, M, dt, e)
+    return ql
+
+
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_small_shapes(orc, fmt):
+    N, K = (256, 1024) if not fmt.startswith("gptq4_row") else (80, 1000)
+    _run(orc, fmt, N, K, [1, 3, 16, 17, 64, 100])
+
+
+def test_dtypes_and_bias(orc):
+    _run(orc, "gptq4", 128, 512, [1, 7], dtypes=("f32", "bf16", "f16"), bias=True)
+    _run(orc, "w8", 128, 512, [2], dtypes=("f32", "f16"), bias=True)
+
+
+def test_ragged_n_and_k(orc):
+    # N not a multiple of 16 and K not a multiple of 128: padded tiles must not leak
+    _run(orc, "gptq4", 72, 384, [1, 5])
+    _run(orc, "mxfp4", 40, 160, [1, 3])
+    _run(orc, "w8", 50, 100, [1, 9])
+
+
+def test_marlin_equals_natural(orc):
+    """A Marlin repack of identical codes gives the identical device result (bit for bit)."""
+    import torch
+    import sgl_qlinear as q
+    kind, a = build("marlin4_asym", 256, 1024, seed=11)
+    mar = product(kind, a, 256, 1024)
+    c, z, s = a["natural"]
+    qw, qz = synth.gptq_pack(c, z)
+    nat = q.QLinear.from_awq_gptq(q.make_cfg(method=2, bits=4, group_size=128, zero_point=1), qw,
+                                  s, 256, 1024, qzeros=qz)
+    A = torch.from_numpy(synth.normal(12, (8, 1024))).cuda()
+    assert torch.equal(mar.forward(A), nat.forward(A))
+    assert torch.equal(mar.dequant(), nat.dequant())
+
+
+@pytest.mark.parametrize("shape", [(11008, 4096), (4096, 11008)])
+def test_gptq_llama7b_mlp(orc, shape):
+    """BASELINE config 2 at full size, M = 1 and 16, f32 and bf16 activations."""
+    _run(orc, "gptq4", shape[0], shape[1], [1, 16], seed=0x5EED0002)
+
+
+def test_w8_qwen05_mlp(orc):
+    """BASELINE config 1 at full size: [4864, 896], M = 1 and 8, f32 activations."""
+    _run(orc, "w8", 4864, 896, [1, 8], dtypes=("f32",), seed=0x5EED0001)
+
+
+def test_mxfp4_8192(orc):
+    """BASELINE config 4 at full size, M = 1 and 16, bf16 activations."""
+    _run(orc, "mxfp4", 8192, 8192, [1, 16], dtypes=("bf16",), seed=0x5EED0004)
