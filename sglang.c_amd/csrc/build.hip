@@ -119,7 +119,7 @@ struct MetaArgs {
 };
 
 __global__ void k_decode_meta(MetaArgs a, const uint32_t *__restrict__ qz,
-                              const float *__restrict__ sc, uint8_t *__restrict__ dz,
+                              const float *__restrict__ sc, uint16_t *__restrict__ dz,
                               float *__restrict__ ds) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= a.ngroups * a.N) return;
@@ -162,7 +162,7 @@ __global__ void k_decode_meta(MetaArgs a, const uint32_t *__restrict__ qz,
       s = sc[n];
       break;
   }
-  dz[i] = (uint8_t)z;  // v2 may give 16: still fits the u8 zero store
+  dz[i] = (uint16_t)z;  // gptq_v2 8-bit may give 256
   ds[i] = s;
 }
 
@@ -211,76 +211,68 @@ __global__ void k_pack_codes(const uint8_t *__restrict__ dc, int64_t N, int64_t 
   out[i] = o;
 }
 
-__global__ void k_pack_meta(const uint8_t *__restrict__ dz, const float *__restrict__ ds,
-                            int64_t N, int64_t ngroups, int64_t ntile, int64_t gpad, int f16,
-                            void *__restrict__ os, uint8_t *__restrict__ oz) {
+// Per-(tile, column, unit) meta entries (layout in sglq_dev.hpp).  A unit is group u
+// (META_GROUP) or step u, whose group is u / spg (META_STEP).
+__global__ void k_pack_meta(const uint16_t *__restrict__ dz, const float *__restrict__ ds,
+                            int64_t N, int64_t ngroups, int64_t ntile, int64_t nmeta,
+                            int64_t upg, int f16, void *__restrict__ om) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= ntile * gpad * 16) return;
-  const int64_t t = i / (gpad * 16), g = (i / 16) % gpad;
-  const int64_t n = t * 16 + (i & 15);
+  if (i >= ntile * 16 * nmeta) return;
+  const int64_t tc = i / nmeta, u = i % nmeta;
+  const int64_t n = (tc >> 4) * 16 + (tc & 15);
+  const int64_t g = u / upg;
   float s = 0.f;
-  uint8_t z = 0;
+  int z = 0;
   if (n < N && g < ngroups) {
     s = ds[g * N + n];
     z = dz[g * N + n];
   }
-  if (f16)
-    ((_Float16 *)os)[i] = (_Float16)s;
-  else
-    ((float *)os)[i] = s;
-  oz[i] = z;
+  const _Float16 zoff = (_Float16)(-1024.0f - (float)z);  // exact: |1024 + z| < 2048
+  const uint32_t zb = (uint32_t)__builtin_bit_cast(uint16_t, zoff);
+  if (f16) {
+    const uint32_t sb = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)s);
+    ((uint32_t *)om)[i] = sb | (zb << 16);
+  } else {
+    ((uint64_t *)om)[i] = (uint64_t)__float_as_uint(s) | ((uint64_t)zb << 32);
+  }
 }
 
-// e8m0 bytes [N][nb] -> [t][chunk][16] u32 (byte j = step 4c + j)
+// e8m0 bytes [N][nb] -> [t][16][nsteps] (step s of the device K is block s)
 __global__ void k_pack_e8m0(const uint8_t *__restrict__ se, int64_t N, int64_t nb, int64_t ntile,
-                            int64_t nchunk, uint32_t *__restrict__ out) {
+                            int64_t nsteps, uint8_t *__restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= ntile * nchunk * 16) return;
-  const int64_t t = i / (nchunk * 16), c = (i / 16) % nchunk;
-  const int64_t n = t * 16 + (i & 15);
-  uint32_t w = 0;
-  if (n < N)
-    for (int j = 0; j < 4; j++) {
-      const int64_t s = c * 4 + j;
-      if (s < nb) w |= (uint32_t)se[n * nb + s] << (8 * j);
-    }
-  out[i] = w;
+  if (i >= ntile * 16 * nsteps) return;
+  const int64_t tc = i / nsteps, s = i % nsteps;
+  const int64_t n = (tc >> 4) * 16 + (tc & 15);
+  out[i] = (n < N && s < nb) ? se[n * nb + s] : (uint8_t)0;
 }
 
 // ---------------------------------------------------------------------------------------
 // exact dequant of the tile layout: out[n*K + k] = (float)(q - z) * s  (U4/U8)
 //                                                = e2m1(q) * (e == 255 ? 0 : 2^(e-127)) (E2M1)
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ float e2m1_value(uint32_t c) {
-  // reference src/qweight.c:325-329
-  const float mag[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
-  const float v = mag[c & 7];
-  return (c & 8) ? -v : v;
-}
-
 struct DqArgs {
-  int kind, scf16;
-  int64_t N, K, nchunk, spc, spg, gpad;
+  int kind, scf16, meta_mode;
+  int64_t N, K, nchunk, spc, cpg, nmeta, nsteps;
 };
 
 __global__ void k_dequant(DqArgs a, const u32x4_t *__restrict__ codes,
-                          const void *__restrict__ scales, const uint8_t *__restrict__ zeros,
-                          const int32_t *__restrict__ kinv, float *__restrict__ out) {
+                          const void *__restrict__ meta, const int32_t *__restrict__ kinv,
+                          float *__restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= a.N * a.K) return;
   const int64_t n = i / a.K, k = i % a.K;
   const int64_t kp = kinv[k];
   const int64_t s = kp >> 5, c = s / a.spc, j = s % a.spc;
-  const int64_t t = n >> 4;
+  const int64_t t = n >> 4, col = (t << 4) + (n & 15);  // == n; meta rows are [t][16]
   const int lane = (int)(((kp & 31) >> 3) * 16 + (n & 15));
   const int e = (int)(kp & 7);
   const u32x4_t blk = codes[(t * a.nchunk + c) * 64 + lane];
   if (a.kind == SGLQ_KIND_E2M1) {
     const uint32_t q = (blk[j] >> (4 * e)) & 15u;
-    const uint32_t ex = (((const uint32_t *)scales)[(t * a.nchunk + c) * 16 + (n & 15)] >>
-                         (8 * j)) & 255u;
+    const uint32_t ex = ((const uint8_t *)meta)[col * a.nsteps + s];
     const float sc = ex == 255 ? 0.f : ldexpf(1.0f, (int)ex - 127);
-    out[i] = e2m1_value(q) * sc;
+    out[i] = sglq_e2m1_value(q) * sc;
     return;
   }
   uint32_t q;
@@ -288,11 +280,21 @@ __global__ void k_dequant(DqArgs a, const u32x4_t *__restrict__ codes,
     q = (blk[2 * j + (e >> 2)] >> (8 * (e & 3))) & 255u;
   else
     q = (blk[j] >> (4 * e)) & 15u;
-  const int64_t g = s / a.spg;
-  const int64_t mi = (t * a.gpad + g) * 16 + (n & 15);
-  const float sc = a.scf16 ? (float)((const _Float16 *)scales)[mi] : ((const float *)scales)[mi];
-  const int qz = (int)q - (int)zeros[mi];
-  out[i] = (float)qz * sc;
+  const int64_t u = a.meta_mode == SGLQ_META_GROUP ? c / a.cpg : s;
+  const int64_t mi = col * a.nmeta + u;
+  float sc;
+  uint16_t zb;
+  if (a.scf16) {
+    const uint32_t m = ((const uint32_t *)meta)[mi];
+    sc = (float)__builtin_bit_cast(_Float16, (uint16_t)(m & 0xFFFFu));
+    zb = (uint16_t)(m >> 16);
+  } else {
+    const uint64_t m = ((const uint64_t *)meta)[mi];
+    sc = __uint_as_float((uint32_t)m);
+    zb = (uint16_t)(m >> 32);
+  }
+  const int z = (int)(-(float)__builtin_bit_cast(_Float16, zb)) - 1024;
+  out[i] = (float)((int)q - z) * sc;  // reference src/qweight.c:102-103, 137-138
 }
 
 // ---------------------------------------------------------------------------------------
@@ -313,7 +315,8 @@ static sglq_dev *build_impl(const sglq_plan *p, const void *qw, const void *qz, 
                             int dev, int on_device) {
   sglq_dev *d = (sglq_dev *)calloc(1, sizeof(sglq_dev));
   void *b_qw = nullptr, *b_qz = nullptr, *b_sc = nullptr;
-  uint8_t *dc = nullptr, *dz = nullptr;
+  uint8_t *dc = nullptr;
+  uint16_t *dz = nullptr;
   float *ds = nullptr;
   int *flag = nullptr;
   hipMemcpyKind kind = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
@@ -330,7 +333,19 @@ static sglq_dev *build_impl(const sglq_plan *p, const void *qw, const void *qz, 
   d->nchunk = p->nsteps / d->spc;
   d->spg = p->gp / 32;
   d->ngroups = p->ngroups;
-  d->gpad = (p->nsteps + d->spg - 1) / d->spg;
+  if (p->kind == SGLQ_KIND_E2M1) {
+    d->meta_mode = SGLQ_META_E8M0;
+    d->nmeta = d->nsteps;
+  } else if (d->spg % d->spc == 0) {
+    d->meta_mode = SGLQ_META_GROUP;  // every group is cpg whole chunks
+    d->cpg = d->spg / d->spc;
+    d->nmeta = (d->nsteps + d->spg - 1) / d->spg;
+  } else {
+    d->meta_mode = SGLQ_META_STEP;
+    d->nmeta = d->nsteps;
+  }
+  d->kident = 1;
+  for (int64_t k = 0; k < p->K && d->kident; k++) d->kident = p->kmap[k] == k;
   SGLQ_HIP(hipSetDevice(dev));
   {
     const int64_t qwb = src_bytes_qweight(p), scb = src_bytes_scales(p);
@@ -381,13 +396,14 @@ static sglq_dev *build_impl(const sglq_plan *p, const void *qw, const void *qz, 
         dc, p->N, p->K, d->kmap, p->kind, d->ntile, d->nchunk, d->codes);
     SGLQ_HIP(hipGetLastError());
     if (p->kind == SGLQ_KIND_E2M1) {
-      SGLQ_HIP(hipMalloc(&d->scales, d->ntile * d->nchunk * 16 * 4));
-      k_pack_e8m0<<<sglq_blocks(d->ntile * d->nchunk * 16, T), T>>>(
-          (const uint8_t *)b_sc, p->N, p->sc_cols, d->ntile, d->nchunk, (uint32_t *)d->scales);
+      const int64_t nm = d->ntile * 16 * d->nsteps;
+      SGLQ_HIP(hipMalloc(&d->meta, nm));
+      k_pack_e8m0<<<sglq_blocks(nm, T), T>>>((const uint8_t *)b_sc, p->N, p->sc_cols, d->ntile,
+                                             d->nsteps, (uint8_t *)d->meta);
       SGLQ_HIP(hipGetLastError());
     } else {
       const int64_t GN = p->ngroups * p->N;
-      SGLQ_HIP(hipMalloc(&dz, GN));
+      SGLQ_HIP(hipMalloc(&dz, GN * 2));
       SGLQ_HIP(hipMalloc(&ds, GN * 4));
       MetaArgs ma = {p->src, p->bits, p->has_zero && qz, p->zconst, p->v2,
                      p->N, p->ngroups, p->qz_cols, p->sc_cols};
@@ -400,15 +416,16 @@ static sglq_dev *build_impl(const sglq_plan *p, const void *qw, const void *qz, 
       int hflag = 1;
       SGLQ_HIP(hipMemcpy(&hflag, flag, 4, hipMemcpyDeviceToHost));
       d->scf16 = hflag == 0;
-      const int64_t nm = d->ntile * d->gpad * 16;
-      SGLQ_HIP(hipMalloc(&d->scales, nm * (d->scf16 ? 2 : 4)));
-      SGLQ_HIP(hipMalloc(&d->zeros, nm));
-      k_pack_meta<<<sglq_blocks(nm, T), T>>>(dz, ds, p->N, p->ngroups, d->ntile, d->gpad,
-                                             d->scf16, d->scales, d->zeros);
+      const int64_t nm = d->ntile * 16 * d->nmeta;
+      SGLQ_HIP(hipMalloc(&d->meta, nm * (d->scf16 ? 4 : 8)));
+      k_pack_meta<<<sglq_blocks(nm, T), T>>>(
+          dz, ds, p->N, p->ngroups, d->ntile, d->nmeta,
+          d->meta_mode == SGLQ_META_GROUP ? 1 : d->spg, d->scf16, d->meta);
       SGLQ_HIP(hipGetLastError());
     }
     SGLQ_HIP(hipDeviceSynchronize());
   }
+  if (sglq_gemv_setup(d) != 0) goto fail;
   (void)hipFree(b_qw);
   (void)hipFree(b_qz);
   (void)hipFree(b_sc);
@@ -443,8 +460,9 @@ extern "C" void sglq_free(sglq_dev *d) {
   if (!d) return;
   (void)hipSetDevice(d->dev);
   (void)hipFree(d->codes);
-  (void)hipFree(d->scales);
-  (void)hipFree(d->zeros);
+  (void)hipFree(d->meta);
+  (void)hipFree(d->gv_part);
+  (void)hipFree(d->gv_cnt);
   (void)hipFree(d->kmap);
   (void)hipFree(d->kinv);
   (void)hipFree(d->ws);
@@ -465,10 +483,11 @@ int sglq_ws_reserve(sglq_dev *d, size_t bytes) {
 }
 
 extern "C" int sglq_dequant_dev(sglq_dev *d, float *out, void *stream) {
-  DqArgs a = {d->kind, d->scf16, d->N, d->K, d->nchunk, d->spc, d->spg, d->gpad};
+  DqArgs a = {d->kind, d->scf16, d->meta_mode, d->N, d->K, d->nchunk, d->spc, d->cpg,
+              d->nmeta, d->nsteps};
   SGLQ_HIP(hipSetDevice(d->dev));
   k_dequant<<<sglq_blocks(d->N * d->K, 256), 256, 0, (hipStream_t)stream>>>(
-      a, d->codes, d->scales, d->zeros, d->kinv, out);
+      a, d->codes, d->meta, d->kinv, out);
   SGLQ_HIP(hipGetLastError());
   return 0;
 fail:
@@ -493,6 +512,7 @@ extern "C" int64_t sglq_N(const sglq_dev *d) { return d->N; }
 extern "C" int64_t sglq_K(const sglq_dev *d) { return d->K; }
 extern "C" int64_t sglq_weight_bytes(const sglq_dev *d) {
   const int64_t codes = d->ntile * d->nchunk * 1024;
-  if (d->kind == SGLQ_KIND_E2M1) return codes + d->ntile * d->nchunk * 64;
-  return codes + d->ntile * d->gpad * 16 * ((d->scf16 ? 2 : 4) + 1);
+  const int64_t nm = d->ntile * 16 * d->nmeta;
+  if (d->kind == SGLQ_KIND_E2M1) return codes + nm;
+  return codes + nm * (d->scf16 ? 4 : 8);
 }

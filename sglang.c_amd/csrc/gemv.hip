@@ -1,76 +1,75 @@
-// gemv.hip — decode-side quantized linear, C[M,N] = A[M,K] * W^T (+ bias), M <= 64 per launch.
+// gemv.hip — decode-side quantized linear, C[M,N] = A[M,K] * W^T (+ bias) for M <= 16.
 //
-// The weight is streamed once from HBM in the tile layout (sglq_dev.hpp): each wave loads
-// 1 KiB per chunk with one 128-bit load per lane, unpacks the codes in registers straight
-// into the B operand of v_mfma_f32_16x16x32_f16 and subtracts the zero exactly in f16
+// Work split: a workgroup is 4 waves; wave w owns the 16-column tile t = 4*cg + w, and all four
+// waves walk the same K range (CPW chunks), so the activations of that range are staged once
+// per workgroup in LDS.  The grid is (column groups) x (K ranges); K ranges of one column group
+// leave fp32 partial sums in a per-handle buffer and the last workgroup to arrive (an arrival
+// counter per column group) adds them in K order and writes C.  No atomics touch C, so the
+// result is deterministic, and every counter is back at zero when a launch ends.
+//
+// Weight codes are streamed once with one 128-bit non-temporal load per lane per chunk, all
+// of a wave's chunks issued before any is consumed.  Codes are unpacked in registers straight
+// into the B operand of v_mfma_f32_16x16x32_f16 with the zero subtracted exactly in f16
 // (q - z is a small integer), so the fp32 MFMA accumulation sees exact weight codes.  The
-// per-(group, column) scale is applied in fp32 when a group ends (e8m0 block scale per step
-// for MXFP4).  A workgroup owns one 16-column tile; its waves split K and are reduced through
-// LDS, so no atomics and a deterministic result.
+// group scale is applied in fp32 per chunk (per step for MXFP4's e8m0 block scales and for
+// group sizes that are not whole chunks).
 //
-// Activations are prepared once per call by k_prep: gathered through kmap (act-order), scaled
-// by an exact per-row power of two so they sit well inside f16 range, and split into f16
-// hi + lo parts when they come in as f32 (hi + lo carries ~22 bits, so the f32 input is kept),
-// laid out per step exactly as the MFMA A operand wants them.
+// Activations: each workgroup finds, per row, the largest |a| over its K range and scales the
+// row by an exact power of two so it sits well inside f16 range; f32 inputs are split into f16
+// hi + lo parts (about 22 significant bits), bf16/f16 inputs fit one f16 part.  The power of
+// two is undone exactly on the partial sum.
 #include "sglq_dev.hpp"
 
-struct PrepArgs {
-  const void *A;
-  int dt;
-  int64_t lda, K, Kp, M;
-  const int32_t *kmap;
-  int perm4;  // U4 operand order: element i holds k-offset {0,4,1,5,2,6,3,7}[i]
-  int split;
-  _Float16 *hi, *lo;
-  int *rowexp;
-};
+namespace {
 
-__device__ __forceinline__ float load_act(const void *A, int dt, int64_t idx) {
-  if (dt == SGLQ_DT_F32) return ((const float *)A)[idx];
-  if (dt == SGLQ_DT_F16) return (float)((const _Float16 *)A)[idx];
-  const uint32_t b = ((const uint16_t *)A)[idx];
-  return __uint_as_float(b << 16);
-}
-
-__global__ __launch_bounds__(256) void k_prep(PrepArgs p) {
-  const int64_t m = blockIdx.x;
-  __shared__ float red[256];
-  float amax = 0.f;
-  for (int64_t k = threadIdx.x; k < p.K; k += 256)
-    amax = fmaxf(amax, fabsf(load_act(p.A, p.dt, m * p.lda + k)));
-  red[threadIdx.x] = amax;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if ((int)threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
-    __syncthreads();
-  }
-  amax = red[0];
-  // exact power-of-two row scale: amax * 2^-e lands in [2^13, 2^14)
-  const int e = (amax > 0.f && amax <= 3.0e38f) ? ilogbf(amax) - 13 : 0;
-  if (threadIdx.x == 0) p.rowexp[m] = e;
-  for (int64_t kp = threadIdx.x; kp < p.Kp; kp += 256) {
-    const int32_t k = p.kmap[kp];
-    const float v = k >= 0 ? ldexpf(load_act(p.A, p.dt, m * p.lda + k), -e) : 0.f;
-    const _Float16 h = (_Float16)v;
-    const int64_t s = kp >> 5;
-    const int r = (int)(kp & 31), kq = r >> 3, o = r & 7;
-    const int i = p.perm4 ? 2 * (o & 3) + (o >> 2) : o;
-    const int64_t idx = ((s * 4 + kq) * p.M + m) * 8 + i;
-    p.hi[idx] = h;
-    if (p.split) p.lo[idx] = (_Float16)(v - (float)h);
-  }
-}
+constexpr int kWaves = 4;
 
 struct GemvArgs {
   const u32x4_t *codes;
-  const void *scales;
-  const uint8_t *zeros;
-  const _Float16 *ahi, *alo;
-  const int *rowexp;
+  const void *meta;
+  const void *A;
+  const int32_t *kmap;  // device position -> original k; nullptr = identity on [0, K)
   const float *bias;
   float *C;
-  int64_t N, M, ldc, nchunk, spg, gpad, m0;
+  float *part;  // [S][M][N]
+  int *cnt;     // [ncg]
+  int64_t lda, ldc;
+  int N, K, M, adt, ntile, nchunk, nmeta, cpg, S, ncg;
 };
+
+__device__ __forceinline__ float bf16_bits(uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ float f16_bits(uint32_t b) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+}
+
+__device__ __forceinline__ float act1(const void *A, int dt, int64_t i) {
+  if (dt == SGLQ_DT_F32) return ((const float *)A)[i];
+  const uint32_t b = ((const uint16_t *)A)[i];
+  return dt == SGLQ_DT_BF16 ? bf16_bits(b) : f16_bits(b);
+}
+
+// Activations of row m at device positions kp .. kp+7 (0 outside [0, K) and in padding), one
+// element at a time (the general path: act-order gather, unaligned rows, K % 8 != 0).
+__device__ __forceinline__ void load8(const GemvArgs &a, int m, int kp, float v[8]) {
+  const int64_t rb = (int64_t)m * a.lda;
+  if (a.kmap == nullptr) {
+#pragma unroll
+    for (int o = 0; o < 8; o++) v[o] = kp + o < a.K ? act1(a.A, a.adt, rb + kp + o) : 0.f;
+  } else {
+#pragma unroll
+    for (int o = 0; o < 8; o++) {
+      const int k = a.kmap[kp + o];
+      v[o] = k >= 0 ? act1(a.A, a.adt, rb + k) : 0.f;
+    }
+  }
+}
+
+// (x & m) | o as one v_and_or_b32 (the compiler otherwise emits an AND and an OR)
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(o));
+  return r;
+}
 
 union H8 {
   half8_t v;
@@ -78,17 +77,22 @@ union H8 {
   half2_t h[4];
 };
 
+// Codes of step j of a chunk -> B operand.  U4 element order is nibbles {0,4,1,5,2,6,3,7}:
+// (x & 0x000F000F) | 0x6400 gives 1024 + q, (x & 0x00F000F0) | 0x5400 gives 64 + q, and the
+// matching exact offsets zA = -(1024 + z), zB = -(64 + z) leave q - z.
 template <int KIND>
-__device__ __forceinline__ half8_t unpack(const u32x4_t &w, int j, half2_t zz) {
+__device__ __forceinline__ half8_t unpack(const u32x4_t &w, int j, half2_t zA, half2_t zB) {
   H8 r;
   if constexpr (KIND == SGLQ_KIND_U4) {
-    const uint32_t x = w[j];
-    r.u[0] = (x & 0x000F000Fu) | 0x64006400u;  // 1024 + q, pairs (0,4)
-    r.u[1] = ((x >> 4) & 0x000F000Fu) | 0x64006400u;   // (1,5)
-    r.u[2] = ((x >> 8) & 0x000F000Fu) | 0x64006400u;   // (2,6)
-    r.u[3] = ((x >> 12) & 0x000F000Fu) | 0x64006400u;  // (3,7)
-#pragma unroll
-    for (int i = 0; i < 4; i++) r.h[i] = r.h[i] + zz;  // exact q - z
+    const uint32_t x = w[j], y = x >> 8;
+    r.u[0] = and_or(x, 0x000F000Fu, 0x64006400u);
+    r.u[1] = and_or(x, 0x00F000F0u, 0x54005400u);
+    r.u[2] = and_or(y, 0x000F000Fu, 0x64006400u);
+    r.u[3] = and_or(y, 0x00F000F0u, 0x54005400u);
+    r.h[0] = r.h[0] + zA;
+    r.h[1] = r.h[1] + zB;
+    r.h[2] = r.h[2] + zA;
+    r.h[3] = r.h[3] + zB;
   } else if constexpr (KIND == SGLQ_KIND_U8) {
     const uint32_t x0 = w[2 * j], x1 = w[2 * j + 1];
     r.u[0] = __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u);  // 1024 + b0, 1024 + b1
@@ -96,7 +100,7 @@ __device__ __forceinline__ half8_t unpack(const u32x4_t &w, int j, half2_t zz) {
     r.u[2] = __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u);
     r.u[3] = __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u);
 #pragma unroll
-    for (int i = 0; i < 4; i++) r.h[i] = r.h[i] + zz;
+    for (int i = 0; i < 4; i++) r.h[i] = r.h[i] + zA;
   } else {
     const uint32_t x = w[j];
     r.h[0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(x, 1.0f, 0);
@@ -107,163 +111,416 @@ __device__ __forceinline__ half8_t unpack(const u32x4_t &w, int j, half2_t zz) {
   return r.v;
 }
 
-template <int KIND, int MT, bool SPLIT, bool SCF16>
-__global__ __launch_bounds__(1024) void k_gemv(GemvArgs a) {
-  extern __shared__ float red[];  // [nw][MT*4][64]
-  constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
-  constexpr int CB = 8;
-  const int64_t t = blockIdx.x;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-  const int n16 = lane & 15, kq = lane >> 4;
-  const int64_t c0 = a.nchunk * w / nw, c1 = a.nchunk * (w + 1) / nw;
-  const int64_t s_last = c1 * SPC - 1;
-  float4_t acc[MT], tmp[MT];
-#pragma unroll
-  for (int i = 0; i < MT; i++) {
-    acc[i] = (float4_t){0.f, 0.f, 0.f, 0.f};
-    tmp[i] = acc[i];
+template <bool SCF16>
+using meta_t = typename std::conditional<SCF16, uint32_t, uint64_t>::type;
+
+template <bool SCF16>
+__device__ __forceinline__ void decode_meta(meta_t<SCF16> m, float &sc, half2_t &zA,
+                                            half2_t &zB) {
+  uint32_t zb;
+  if constexpr (SCF16) {
+    sc = f16_bits(m & 0xFFFFu);
+    zb = m >> 16;
+  } else {
+    sc = __uint_as_float((uint32_t)m);
+    zb = (uint32_t)(m >> 32) & 0xFFFFu;
   }
-  const u32x4_t *cp = a.codes + t * a.nchunk * 64 + lane;
-  const uint32_t *ep = (const uint32_t *)a.scales + t * a.nchunk * 16 + n16;
-  int64_t gcur = -1;
-  half2_t zz = {(_Float16)0, (_Float16)0};
-  float sc = 0.f;
-  for (int64_t cb = c0; cb < c1; cb += CB) {
-    u32x4_t wv[CB];
-    uint32_t ev[CB];
+  const _Float16 z = __builtin_bit_cast(_Float16, (uint16_t)zb);
+  zA = (half2_t){z, z};
+  const _Float16 z2 = z + (_Float16)960.0f;  // -(64 + zero), exact
+  zB = (half2_t){z2, z2};
+}
+
+// element i of a U4 operand holds k-offset {0,4,1,5,2,6,3,7}[i]
+__device__ __forceinline__ constexpr int kofs4(int i) { return (i >> 1) + 4 * (i & 1); }
+
+template <int KIND, int CPW, bool SPLIT, bool SCF16, bool STEPM, bool FAST>
+__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+  constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
+  constexpr int SL = CPW * SPC;  // steps in one K range
+  constexpr int IPR = SL * 4;    // 8-element activation items per row
+  constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
+  constexpr int RS = IPR + 1;    // LDS row stride in 16-B items (+1 spreads rows over banks)
+  extern __shared__ half8_t s_act[];  // [SPLIT ? 2 : 1][M][RS]
+  __shared__ unsigned s_amax[16];
+  __shared__ int s_exp[16];
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int cg = (int)(blockIdx.x % (unsigned)a.ncg), sidx = (int)(blockIdx.x / (unsigned)a.ncg);
+  const int c0 = sidx * CPW;
+  const int nc = min(CPW, a.nchunk - c0);
+  const int kp0 = c0 * SPC * 32;
+  const int M = a.M;
+  const int items = M * IPR;
+  const int t = cg * kWaves + w;
+  const bool tvalid = t < a.ntile;
+  const int tl = min(t, a.ntile - 1);  // waves past the last tile load valid memory, unused
+  const int n16 = lane & 15, kq = lane >> 4;
+
+  // ---- activations of this K range: the first two 8-element items of every thread are
+  // loaded before the weight loads (vmcnt retires in order, so they can be consumed while the
+  // weights are still in flight) and stay in registers until they are converted
+  if (tid < 16) s_amax[tid] = 0u;
+  // raw 8-element items: FAST loads are one (16-bit) or two (f32) 128-bit loads from a clamped,
+  // always-valid address with no branch; decoding to f32 happens at first use
+  constexpr int RW = SPLIT ? 2 : 1;
+  struct Raw {
+    u32x4_t q[RW];
+    bool ok;
+  };
+  auto load_raw = [&](int it, Raw &x) {
+    const int m = it / IPR, r = it % IPR;
+    const int kp = kp0 + (r >> 2) * 32 + (r & 3) * 8;
+    x.ok = (r >> 2) < nc * SPC && it < items && (!FAST || kp < a.K);
+    if constexpr (FAST) {
+      const int64_t off = (int64_t)min(m, M - 1) * a.lda + (x.ok ? kp : 0);
+      const u32x4_t *p = (const u32x4_t *)((const char *)a.A + off * (SPLIT ? 4 : 2));
 #pragma unroll
-    for (int i = 0; i < CB; i++)
-      if (cb + i < c1) {
-        wv[i] = __builtin_nontemporal_load(cp + (cb + i) * 64);
-        if constexpr (KIND == SGLQ_KIND_E2M1) ev[i] = ep[(cb + i) * 16];
+      for (int i = 0; i < RW; i++) x.q[i] = p[i];
+    }
+  };
+  auto decode_raw = [&](int it, const Raw &x, float (&v)[8]) {
+#pragma unroll
+    for (int o = 0; o < 8; o++) v[o] = 0.f;
+    if (!x.ok) return;
+    if constexpr (FAST) {
+      if constexpr (SPLIT) {
+#pragma unroll
+        for (int o = 0; o < 8; o++) v[o] = __uint_as_float(x.q[o >> 2][o & 3]);
+      } else if (a.adt == SGLQ_DT_BF16) {
+#pragma unroll
+        for (int o = 0; o < 8; o++) v[o] = bf16_bits((x.q[0][o >> 1] >> (16 * (o & 1))) & 0xFFFFu);
+      } else {
+#pragma unroll
+        for (int o = 0; o < 8; o++) v[o] = f16_bits((x.q[0][o >> 1] >> (16 * (o & 1))) & 0xFFFFu);
       }
+    } else {
+      const int m = it / IPR, r = it % IPR;
+      load8(a, m, kp0 + (r >> 2) * 32 + (r & 3) * 8, v);
+    }
+  };
+  auto load_item = [&](int it, float (&v)[8]) {
+    Raw x;
+    load_raw(it, x);
+    decode_raw(it, x, v);
+  };
+  auto amax_item = [&](int it, const float (&v)[8]) {
+    float mx = 0.f;
 #pragma unroll
-    for (int i = 0; i < CB; i++) {
-      if (cb + i >= c1) break;
+    for (int o = 0; o < 8; o++) mx = fmaxf(mx, fabsf(v[o]));
+    atomicMax(&s_amax[it / IPR], __float_as_uint(mx));
+  };
+  auto store_item = [&](int it, const float (&v)[8]) {
+    const int m = it / IPR, r = it % IPR;
+    const int e = s_exp[m];
+    half8_t hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float x = ldexpf(v[KIND == SGLQ_KIND_U4 ? kofs4(i) : i], -e);
+      const _Float16 h = (_Float16)x;
+      hi[i] = h;
+      lo[i] = (_Float16)(x - (float)h);
+    }
+    s_act[m * RS + r] = hi;
+    if constexpr (SPLIT) s_act[(M + m) * RS + r] = lo;
+  };
+  Raw keep[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) load_raw(tid + 256 * j, keep[j]);
+
+  // ---- this wave's weight loads (meta, then codes), all issued before the activation
+  // staging so their HBM latency overlaps it.  Indices past the range are clamped to its last chunk (valid
+  // memory, never used), so the loads are straight-line code.
+  constexpr int NMV = E2M1 ? CPW : (STEPM ? CPW * SPC : CPW);
+  using MT = typename std::conditional<E2M1, uint32_t, meta_t<SCF16>>::type;
+  MT mv[NMV];
+  const int64_t mrow = ((int64_t)tl * 16 + n16) * a.nmeta;
+  if constexpr (E2M1) {
+    const uint32_t *ep = (const uint32_t *)((const uint8_t *)a.meta + mrow) + c0;
+#pragma unroll
+    for (int i = 0; i < CPW; i++) mv[i] = ep[min(i, nc - 1)];
+  } else if constexpr (STEPM) {
+    const MT *mp = (const MT *)a.meta + mrow + (int64_t)c0 * SPC;
+#pragma unroll
+    for (int i = 0; i < CPW * SPC; i++) mv[i] = mp[min(i, nc * SPC - 1)];
+  } else {
+    const MT *mp = (const MT *)a.meta + mrow;
+    int g = c0 / a.cpg, r = c0 - g * a.cpg;
+    const int glast = (c0 + nc - 1) / a.cpg;
+#pragma unroll
+    for (int i = 0; i < CPW; i++) {
+      mv[i] = mp[min(g, glast)];
+      if (++r == a.cpg) {
+        r = 0;
+        g++;
+      }
+    }
+  }
+  const u32x4_t *cp = a.codes + ((int64_t)tl * a.nchunk + c0) * 64 + lane;
+  u32x4_t wv[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; i++) wv[i] = __builtin_nontemporal_load(cp + min(i, nc - 1) * 64);
+  __builtin_amdgcn_sched_barrier(0);  // keep the whole batch of loads ahead of the staging
+
+  __syncthreads();  // s_amax cleared
+  float kv[2][8];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    decode_raw(tid + 256 * j, keep[j], kv[j]);
+    if (tid + 256 * j < items) amax_item(tid + 256 * j, kv[j]);
+  }
+  for (int it = tid + 512; it < items; it += 256) {
+    float v[8];
+    load_item(it, v);
+    amax_item(it, v);
+  }
+  __syncthreads();
+  if (tid < M) {
+    const float mx = __uint_as_float(s_amax[tid]);
+    s_exp[tid] = (mx > 0.f && mx <= 3.0e38f) ? ilogbf(mx) - 13 : 0;  // max in [2^13, 2^14)
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+    if (tid + 256 * j < items) store_item(tid + 256 * j, kv[j]);
+  for (int it = tid + 512; it < items; it += 256) {
+    float v[8];
+    load_item(it, v);
+    store_item(it, v);
+  }
+  __syncthreads();
+
+  // ---- multiply
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  {
+    // activation operands of one chunk.  Lanes of rows >= M read row M-1 instead: an A row
+    // only feeds the same row of the product, and rows >= M are never written.
+    constexpr int NP = SPLIT ? 2 : 1;
+    const half8_t *arow_p = s_act + min(n16, M - 1) * RS + kq;
+    auto read_ops = [&](int i, half8_t (&op)[SPC * NP]) {
 #pragma unroll
       for (int j = 0; j < SPC; j++) {
-        const int64_t s = (cb + i) * SPC + j;
-        if constexpr (KIND != SGLQ_KIND_E2M1) {
-          const int64_t g = s / a.spg;
-          if (g != gcur) {
-            gcur = g;
-            const int64_t mi = (t * a.gpad + g) * 16 + n16;
-            sc = SCF16 ? (float)((const _Float16 *)a.scales)[mi] : ((const float *)a.scales)[mi];
-            const _Float16 zh = (_Float16)(-1024.0f - (float)a.zeros[mi]);
-            zz = (half2_t){zh, zh};
-          }
+        op[j] = arow_p[(i * SPC + j) * 4];
+        if constexpr (SPLIT) op[SPC + j] = arow_p[M * RS + (i * SPC + j) * 4];
+      }
+    };
+
+    float4_t t0 = {0.f, 0.f, 0.f, 0.f};
+    half8_t opc[SPC * NP], opn[SPC * NP];
+    read_ops(0, opc);
+#pragma unroll
+    for (int i = 0; i < CPW; i++) {
+      // chunks past the range (i >= nc) run on zero activations with a zero scale: straight-
+      // line code keeps every load ahead of the arithmetic
+      const bool live = i < nc;
+      if (i + 1 < CPW) read_ops(i + 1, opn);
+      float sc = 0.f;
+      half2_t zA = {0, 0}, zB = {0, 0};
+      if constexpr (!E2M1 && !STEPM) {
+        decode_meta<SCF16>(mv[i], sc, zA, zB);
+        sc = live ? sc : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < SPC; j++) {
+        if constexpr (!E2M1 && STEPM) {
+          decode_meta<SCF16>(mv[i * SPC + j], sc, zA, zB);
+          sc = live ? sc : 0.f;
         }
-        const half8_t b = unpack<KIND>(wv[i], j, zz);
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-          const int64_t m = mt * 16 + n16;
-          half8_t av = {0, 0, 0, 0, 0, 0, 0, 0};
-          const int64_t ai = ((s * 4 + kq) * a.M + m) * 8;
-          if (m < a.M) av = *(const half8_t *)(a.ahi + ai);
-          tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, tmp[mt], 0, 0, 0);
-          if constexpr (SPLIT) {
-            half8_t lv = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (m < a.M) lv = *(const half8_t *)(a.alo + ai);
-            tmp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(lv, b, tmp[mt], 0, 0, 0);
+        const half8_t b = unpack<KIND>(wv[i], j, zA, zB);
+        t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[j], b, t0, 0, 0, 0);
+        if constexpr (SPLIT)
+          t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[SPC + j], b, t0, 0, 0, 0);
+        if constexpr (E2M1 || STEPM) {
+          if constexpr (E2M1) {
+            const uint32_t ex = (mv[i] >> (8 * j)) & 255u;
+            sc = (ex == 255u || !live) ? 0.f : ldexpf(1.0f, (int)ex - 127);  // ref qweight.c:361
           }
+          acc += sc * t0;
+          t0 = (float4_t){0.f, 0.f, 0.f, 0.f};
         }
-        if constexpr (KIND == SGLQ_KIND_E2M1) {
-          const uint32_t ex = (ev[i] >> (8 * j)) & 255u;
-          const float ss = ex == 255 ? 0.f : ldexpf(1.0f, (int)ex - 127);
+      }
+      if constexpr (!E2M1 && !STEPM) {
+        acc += sc * t0;
+        t0 = (float4_t){0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
-          for (int mt = 0; mt < MT; mt++) {
-            acc[mt] += ss * tmp[mt];
-            tmp[mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-          }
-        } else if ((s + 1) % a.spg == 0 || s == s_last) {
+      for (int q = 0; q < SPC * NP; q++) opc[q] = opn[q];
+    }
+
+    // lane holds rows 4*kq + i of column n (v_mfma_f32_16x16x32 C layout)
+    const int n = t * 16 + n16;
+    if (tvalid && n < a.N) {
 #pragma unroll
-          for (int mt = 0; mt < MT; mt++) {
-            acc[mt] += sc * tmp[mt];
-            tmp[mt] = (float4_t){0.f, 0.f, 0.f, 0.f};
-          }
+      for (int i = 0; i < 4; i++) {
+        const int r = 4 * kq + i;
+        if (r < M) {
+          const float v = ldexpf(acc[i], s_exp[r]);
+          if (a.S == 1)
+            a.C[r * a.ldc + n] = v + (a.bias ? a.bias[n] : 0.f);
+          else  // device-scope store: written through to the level all XCDs share
+            __hip_atomic_store(&a.part[((int64_t)sidx * M + r) * a.N + n], v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         }
       }
     }
   }
-  // cross-wave reduction in a fixed order
-#pragma unroll
-  for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) red[(w * MT * 4 + mt * 4 + r) * 64 + lane] = acc[mt][r];
+  if (a.S == 1) return;
+
+  // ---- split-K: the last workgroup of this column group adds the partials in K order.
+  // The partials are device-scope stores/loads, so no cache write-back or invalidate is
+  // needed; waiting for the stores' acknowledgement before the arrival increment orders them.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
-  for (int idx = threadIdx.x; idx < MT * 4 * 64; idx += blockDim.x) {
-    float sum = 0.f;
-    for (int ww = 0; ww < nw; ww++) sum += red[ww * MT * 4 * 64 + idx];
-    const int e = idx >> 6, l = idx & 63;
-    const int64_t m = (e >> 2) * 16 + 4 * (l >> 4) + (e & 3);
-    const int64_t n = t * 16 + (l & 15);
-    if (m < a.M && n < a.N)
-      a.C[(a.m0 + m) * a.ldc + n] = ldexpf(sum, a.rowexp[m]) + (a.bias ? a.bias[n] : 0.f);
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(&a.cnt[cg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             a.S - 1;
+  __syncthreads();
+  if (!s_last) return;
+  constexpr int NCOL = kWaves * 16;
+  for (int idx = tid; idx < M * NCOL; idx += 256) {
+    const int r = idx / NCOL, n = cg * NCOL + idx % NCOL;
+    if (n < a.N) {
+      float sum = 0.f;
+      for (int s = 0; s < a.S; s++)
+        sum += __hip_atomic_load(&a.part[((int64_t)s * M + r) * a.N + n], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      a.C[r * a.ldc + n] = sum + (a.bias ? a.bias[n] : 0.f);
+    }
+  }
+  if (tid == 0) __hip_atomic_store(&a.cnt[cg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int KIND, int CPW, bool SPLIT, bool FAST>
+void launch4(const GemvArgs &a, int scf16, int stepm, size_t lds, unsigned grid,
+             hipStream_t st) {
+  if constexpr (KIND == SGLQ_KIND_E2M1) {
+    k_gemv<KIND, CPW, SPLIT, true, false, FAST><<<grid, 256, lds, st>>>(a);
+  } else {
+    if (scf16) {
+      if (stepm)
+        k_gemv<KIND, CPW, SPLIT, true, true, FAST><<<grid, 256, lds, st>>>(a);
+      else
+        k_gemv<KIND, CPW, SPLIT, true, false, FAST><<<grid, 256, lds, st>>>(a);
+    } else {
+      if (stepm)
+        k_gemv<KIND, CPW, SPLIT, false, true, FAST><<<grid, 256, lds, st>>>(a);
+      else
+        k_gemv<KIND, CPW, SPLIT, false, false, FAST><<<grid, 256, lds, st>>>(a);
+    }
   }
 }
 
-template <int KIND, int MT, bool SPLIT>
-static void launch_kind(const GemvArgs &a, int scf16, int nw, int64_t ntile, hipStream_t st) {
-  const size_t lds = (size_t)nw * MT * 4 * 64 * 4;
-  if (scf16)
-    k_gemv<KIND, MT, SPLIT, true><<<ntile, nw * 64, lds, st>>>(a);
+template <int KIND, int CPW, bool SPLIT>
+void launch3(const GemvArgs &a, int scf16, int stepm, bool fast, size_t lds, unsigned grid,
+             hipStream_t st) {
+  if (fast)
+    launch4<KIND, CPW, SPLIT, true>(a, scf16, stepm, lds, grid, st);
   else
-    k_gemv<KIND, MT, SPLIT, false><<<ntile, nw * 64, lds, st>>>(a);
+    launch4<KIND, CPW, SPLIT, false>(a, scf16, stepm, lds, grid, st);
 }
 
 template <int KIND>
-static void launch_mt(const GemvArgs &a, int mt, bool split, int scf16, int nw, int64_t ntile,
-                      hipStream_t st) {
-#define SGLQ_L(MTV)                                                  \
-  if (split)                                                         \
-    launch_kind<KIND, MTV, true>(a, scf16, nw, ntile, st);           \
-  else                                                               \
-    launch_kind<KIND, MTV, false>(a, scf16, nw, ntile, st);
-  switch (mt) {
-    case 1: SGLQ_L(1) break;
-    case 2: SGLQ_L(2) break;
-    case 3: SGLQ_L(3) break;
-    default: SGLQ_L(4) break;
+void launch_kind(const GemvArgs &a, int cpw, bool split, int scf16, int stepm, bool fast,
+                 size_t lds, unsigned grid, hipStream_t st) {
+  if (cpw == 8) {
+    if (split)
+      launch3<KIND, 8, true>(a, scf16, stepm, fast, lds, grid, st);
+    else
+      launch3<KIND, 8, false>(a, scf16, stepm, fast, lds, grid, st);
+  } else {
+    if (split)
+      launch3<KIND, 4, true>(a, scf16, stepm, fast, lds, grid, st);
+    else
+      launch3<KIND, 4, false>(a, scf16, stepm, fast, lds, grid, st);
   }
-#undef SGLQ_L
 }
 
-// waves per workgroup: enough that every wave streams at most ~8 KiB of codes
-static int pick_waves(int64_t nchunk) {
-  int nw = 4;
-  while (nw < 16 && nchunk > (int64_t)nw * 8) nw *= 2;
-  return nw;
+constexpr size_t kMaxLds = 48 * 1024;
+
+size_t act_lds(const sglq_dev *d, int cpw, bool split, int64_t M) {
+  return (size_t)(split ? 2 : 1) * (cpw * d->spc * 4 + 1) * M * 16;
+}
+
+}  // namespace
+
+int sglq_gemv_setup(sglq_dev *d) {
+  const int64_t ncg = (d->ntile + kWaves - 1) / kWaves;
+  // 8 chunks (8 KiB of codes per wave) unless that leaves fewer than two workgroups per CU
+  d->gv_cpw = (ncg * ((d->nchunk + 7) / 8) < 512 && d->nchunk > 4) ? 4 : 8;
+  d->gv_split = (int)((d->nchunk + 3) / 4);  // the most K ranges any launch uses (cpw = 4)
+  if (d->gv_split > 1) {
+    SGLQ_HIP(hipMalloc(&d->gv_part, (size_t)d->gv_split * 16 * d->N * sizeof(float)));
+    SGLQ_HIP(hipMalloc(&d->gv_cnt, (size_t)ncg * sizeof(int)));
+    SGLQ_HIP(hipMemset(d->gv_cnt, 0, (size_t)ncg * sizeof(int)));
+  }
+  return 0;
+fail:
+  return -1;
+}
+
+int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
+              float *C, int64_t ldc, hipStream_t st) {
+  const bool split = dt == SGLQ_DT_F32;
+  int cpw = d->gv_cpw;
+  if (act_lds(d, cpw, split, M) > kMaxLds) cpw = 4;
+  const int S = (int)((d->nchunk + cpw - 1) / cpw);
+  const int ncg = (int)((d->ntile + kWaves - 1) / kWaves);
+  const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
+  GemvArgs a;
+  a.codes = d->codes;
+  a.meta = d->meta;
+  a.A = A;
+  a.kmap = d->kident ? nullptr : d->kmap;
+  a.bias = bias;
+  a.C = C;
+  a.part = d->gv_part;
+  a.cnt = d->gv_cnt;
+  a.lda = lda;
+  a.ldc = ldc;
+  a.N = (int)d->N;
+  a.K = (int)d->K;
+  a.M = (int)M;
+  a.adt = dt;
+  a.ntile = (int)d->ntile;
+  a.nchunk = (int)d->nchunk;
+  a.nmeta = (int)d->nmeta;
+  a.cpg = d->cpg > 0 ? (int)d->cpg : 1;
+  a.S = S;
+  a.ncg = ncg;
+  const bool fast = d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
+                    (lda * esz) % 16 == 0;
+  const size_t lds = act_lds(d, cpw, split, M);
+  const unsigned grid = (unsigned)(ncg * S);
+  const int stepm = d->meta_mode == SGLQ_META_STEP;
+  switch (d->kind) {
+    case SGLQ_KIND_U4: launch_kind<SGLQ_KIND_U4>(a, cpw, split, d->scf16, stepm, fast, lds, grid, st); break;
+    case SGLQ_KIND_U8: launch_kind<SGLQ_KIND_U8>(a, cpw, split, d->scf16, stepm, fast, lds, grid, st); break;
+    default: launch_kind<SGLQ_KIND_E2M1>(a, cpw, split, 1, 0, fast, lds, grid, st); break;
+  }
+  SGLQ_HIP(hipGetLastError());
+  return 0;
+fail:
+  return -1;
 }
 
 extern "C" int sglq_forward(sglq_dev *d, const void *A, int dt, int64_t M, const float *bias,
                             float *C, void *stream) {
   hipStream_t st = (hipStream_t)stream;
-  const int64_t Kp = d->nsteps * 32;
-  const bool split = dt == SGLQ_DT_F32;
   const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
-  const int nw = pick_waves(d->nchunk);
   SGLQ_HIP(hipSetDevice(d->dev));
-  for (int64_t m0 = 0; m0 < M; m0 += 64) {
-    const int64_t mb = M - m0 < 64 ? M - m0 : 64;
-    const size_t half_elems = (size_t)(Kp * mb);
-    const size_t need = half_elems * 2 * (split ? 2 : 1) + 64 * 4 + 256;
-    if (sglq_ws_reserve(d, need) != 0) return -1;
-    _Float16 *hi = (_Float16 *)d->ws;
-    _Float16 *lo = hi + half_elems;
-    int *rowexp = (int *)((char *)d->ws + half_elems * 2 * (split ? 2 : 1));
-    PrepArgs pa = {(const char *)A + m0 * d->K * esz, dt, d->K, d->K, Kp, mb, d->kmap,
-                   d->kind == SGLQ_KIND_U4, split, hi, lo, rowexp};
-    k_prep<<<(unsigned)mb, 256, 0, st>>>(pa);
-    SGLQ_HIP(hipGetLastError());
-    GemvArgs ga = {d->codes, d->scales, d->zeros, hi, lo, rowexp, bias, C,
-                   d->N, mb, d->N, d->nchunk, d->spg, d->gpad, m0};
-    const int mt = (int)((mb + 15) / 16);
-    switch (d->kind) {
-      case SGLQ_KIND_U4: launch_mt<SGLQ_KIND_U4>(ga, mt, split, d->scf16, nw, d->ntile, st); break;
-      case SGLQ_KIND_U8: launch_mt<SGLQ_KIND_U8>(ga, mt, split, d->scf16, nw, d->ntile, st); break;
-      default: launch_mt<SGLQ_KIND_E2M1>(ga, mt, split, 0, nw, d->ntile, st); break;
-    }
-    SGLQ_HIP(hipGetLastError());
+  if (d->N > INT32_MAX || d->K > INT32_MAX / 2 || d->ntile * 16 * d->nmeta > INT32_MAX * 4LL) {
+    sglq_log_error("qlinear: N=%lld K=%lld beyond the GEMV's 32-bit indexing", (long long)d->N,
+                   (long long)d->K);
+    return -1;
+  }
+  for (int64_t m0 = 0; m0 < M; m0 += 16) {
+    const int64_t mb = M - m0 < 16 ? M - m0 : 16;
+    if (sglq_gemv(d, (const char *)A + m0 * d->K * esz, dt, d->K, mb, bias, C + m0 * d->N, d->N,
+                  st) != 0)
+      return -1;
   }
   return 0;
 fail:

@@ -5,14 +5,17 @@
 //   * N is cut into tiles of 16 columns (t = n / 16); K is re-indexed through kmap into device
 //     positions k' (act-order groups made contiguous, each group padded to a multiple of 32) and
 //     cut into MFMA steps of 32 (s = k' / 32).
-//   * codes: for every (tile t, chunk c) one 1 KiB block = 64 lanes x 16 B.  Lane l carries
-//     column n = 16t + (l & 15) and k' = 32 s + 8 (l >> 4) + i, i.e. exactly the B operand of
-//     v_mfma_f32_16x16x32_f16 for that step.  4-bit kinds: a chunk is 4 steps, word j of the
-//     lane is step 4c+j, nibble i holds i.  8-bit kind: a chunk is 2 steps, words (2j, 2j+1)
-//     are step 2c+j, byte b of the pair holds i = b.
-//   * U4/U8 meta: scales [t][gpad][16] (f16 when every scale is f16-exact, else f32) and
-//     zeros [t][gpad][16] u8 (the value subtracted from the code).
-//   * E2M1 meta: e8m0 bytes [t][chunk][16] packed 4 steps per u32 (byte j = step 4c+j).
+//   * codes: for every (tile t, chunk c) one 1 KiB block = 64 lanes x 16 B, tiles outermost,
+//     chunks of one tile contiguous.  Lane l carries column n = 16t + (l & 15) and
+//     k' = 32 s + 8 (l >> 4) + i, i.e. exactly the B operand of v_mfma_f32_16x16x32_f16 for that
+//     step.  4-bit kinds: a chunk is 4 steps, word j of the lane is step 4c+j, nibble i holds
+//     k-offset i.  8-bit kind: a chunk is 2 steps, words (2j, 2j+1) are step 2c+j, byte b of
+//     the pair holds k-offset b.
+//   * U4/U8 meta, one entry per (tile, column, unit) stored [t][16][nmeta]; a unit is a group
+//     when every group is a whole number of chunks (META_GROUP, cpg chunks per group), else a
+//     step (META_STEP).  Entry = f16 scale | f16 -(1024 + zero) << 16 when every scale is
+//     f16-exact (4 bytes), else f32 scale | f16 -(1024 + zero) << 32 (8 bytes).
+//   * E2M1 meta: the e8m0 byte of every (column, step), stored [t][16][nsteps] (u8).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -24,25 +27,35 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+enum { SGLQ_META_GROUP = 0, SGLQ_META_STEP = 1, SGLQ_META_E8M0 = 2 };
+
 struct sglq_dev {
   int dev;
-  int kind;    // SGLQ_KIND_*
-  int scf16;   // U4/U8 scales stored as f16
-  int src;     // SGLQ_SRC_* it was built from
+  int kind;       // SGLQ_KIND_*
+  int scf16;      // U4/U8 meta entries hold f16 scales (4 B) rather than f32 (8 B)
+  int src;        // SGLQ_SRC_* it was built from
+  int meta_mode;  // SGLQ_META_*
+  int kident;     // kmap is the identity on [0, K) (no act-order, no padding inside K)
   int64_t N, K;
   int64_t ntile;   // ceil(N / 16)
   int64_t nsteps;  // device K / 32
   int64_t spc;     // steps per chunk (4 for 4-bit kinds, 2 for 8-bit)
   int64_t nchunk;  // nsteps / spc
   int64_t spg;     // steps per group
+  int64_t cpg;     // chunks per group (META_GROUP)
   int64_t ngroups; // real groups
-  int64_t gpad;    // groups stored per tile (>= nsteps / spg)
+  int64_t nmeta;   // meta entries per column
   u32x4_t *codes;
-  void *scales;
-  uint8_t *zeros;
+  void *meta;
   int32_t *kmap;  // [nsteps * 32]
   int32_t *kinv;  // [K]
-  // forward workspace (grown on demand)
+  // decode GEMV split-K state, sized at build: partial sums [gv_split][16][N] and one arrival
+  // counter per group of 4 tiles (every counter is back at 0 when a launch ends)
+  int gv_cpw;      // chunks per wave (4 or 8)
+  int gv_split;    // K ranges per column group
+  float *gv_part;
+  int *gv_cnt;
+  // prefill GEMM workspace (grown on demand)
   void *ws;
   size_t ws_bytes;
 };
@@ -63,3 +76,16 @@ static inline unsigned sglq_blocks(int64_t n, int threads) {
 
 // Grows d->ws to at least `bytes` (device memory, kept for the handle's lifetime).
 int sglq_ws_reserve(sglq_dev *d, size_t bytes);
+
+// Decode-GEMV launch (gemv.hip): C rows [0, M) with M <= 16.
+int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
+              float *C, int64_t ldc, hipStream_t st);
+// Picks the decode GEMV split for a freshly built weight and allocates its state.
+int sglq_gemv_setup(sglq_dev *d);
+
+__device__ __forceinline__ float sglq_e2m1_value(uint32_t c) {
+  // reference src/qweight.c:325-329
+  const float mag[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
+  const float v = mag[c & 7];
+  return (c & 8) ? -v : v;
+}

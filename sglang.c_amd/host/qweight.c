@@ -34,7 +34,8 @@ int qh_plan_groups(sglq_plan *p, int64_t ngroups, const int32_t *gidx, int spc, 
   int64_t gmax = 0;
   for (int64_t g = 0; g < ngroups; g++) gmax = cnt[g] > gmax ? cnt[g] : gmax;
   p->ngroups = ngroups;
-  p->gp = ngroups == 1 ? round_up(K, 32) : round_up(gmax, 32);
+  /* one group (per-channel scale): pad it to whole chunks so its scale is applied per chunk */
+  p->gp = ngroups == 1 ? round_up(K, 32 * spc) : round_up(gmax, 32);
   p->nsteps = round_up(ngroups * p->gp / 32, spc);
   *kmap = (int32_t *)malloc(sizeof(int32_t) * (size_t)(p->nsteps * 32));
   *kinv = (int32_t *)malloc(sizeof(int32_t) * (size_t)K);

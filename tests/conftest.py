@@ -3,6 +3,9 @@ import sys
 
 import numpy as np
 import pytest
+# torch bundles its own HIP runtime under the same SONAME as /opt/rocm's; importing it before any
+# test dlopens libsgl_qlinear.so makes the library bind to that one runtime.
+import torch  # noqa: F401
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "sglang.c_amd")

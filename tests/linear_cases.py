@@ -9,6 +9,8 @@ from oracle.oracle import make_cfg as ocfg
 def build(fmt, N, K, seed=1, G=128):
     """Returns (kind, args dict, oracle-side callable producing f32 W)."""
     W = synth.normal(seed, (N, K), 0.02)
+    if "_g" in fmt and fmt.rsplit("_g", 1)[1].isdigit():  # e.g. gptq4_g32: other group size
+        fmt, G = fmt.rsplit("_g", 1)[0], int(fmt.rsplit("_g", 1)[1])
     if fmt in ("gptq4", "gptq4_act", "gptq4_v2", "gptq4_noz", "gptq8", "gptq4_row"):
         bits = 8 if fmt == "gptq8" else 4
         gi = synth.act_order_gidx(seed + 1, K, G) if fmt == "gptq4_act" else None
