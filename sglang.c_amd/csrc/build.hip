@@ -247,6 +247,19 @@ __global__ void k_pack_e8m0(const uint8_t *__restrict__ se, int64_t N, int64_t n
   out[i] = (n < N && s < nb) ? se[n * nb + s] : (uint8_t)0;
 }
 
+// largest e8m0 byte of each column (255, the reference's "scale 0" code, ignored; 0 if none)
+__global__ void k_col_e8m0_max(const uint8_t *__restrict__ m, int64_t ncol, int64_t nsteps,
+                               uint8_t *__restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= ncol) return;
+  uint32_t mx = 0;
+  for (int64_t s = 0; s < nsteps; s++) {
+    const uint32_t e = m[i * nsteps + s];
+    if (e != 255u && e > mx) mx = e;
+  }
+  out[i] = (uint8_t)mx;
+}
+
 // ---------------------------------------------------------------------------------------
 // exact dequant of the tile layout: out[n*K + k] = (float)(q - z) * s  (U4/U8)
 //                                                = e2m1(q) * (e == 255 ? 0 : 2^(e-127)) (E2M1)
@@ -401,6 +414,10 @@ static sglq_dev *build_impl(const sglq_plan *p, const void *qw, const void *qz, 
       k_pack_e8m0<<<sglq_blocks(nm, T), T>>>((const uint8_t *)b_sc, p->N, p->sc_cols, d->ntile,
                                              d->nsteps, (uint8_t *)d->meta);
       SGLQ_HIP(hipGetLastError());
+      SGLQ_HIP(hipMalloc(&d->colexp, d->ntile * 16));
+      k_col_e8m0_max<<<sglq_blocks(d->ntile * 16, T), T>>>((const uint8_t *)d->meta,
+                                                           d->ntile * 16, d->nsteps, d->colexp);
+      SGLQ_HIP(hipGetLastError());
     } else {
       const int64_t GN = p->ngroups * p->N;
       SGLQ_HIP(hipMalloc(&dz, GN * 2));
@@ -461,6 +478,7 @@ extern "C" void sglq_free(sglq_dev *d) {
   (void)hipSetDevice(d->dev);
   (void)hipFree(d->codes);
   (void)hipFree(d->meta);
+  (void)hipFree(d->colexp);
   (void)hipFree(d->gv_part);
   (void)hipFree(d->gv_cnt);
   (void)hipFree(d->kmap);

@@ -1,0 +1,435 @@
+// gemm.hip — prefill-side quantized linear, C[M,N] = A[M,K] * W^T (+ bias) for M > 16.
+//
+// Two launches:
+//   k_prep_a  one workgroup per row: finds the row's largest |a|, scales the row by an exact
+//             power of two into f16 range and writes it as MFMA A operands (f16 hi, plus lo
+//             for f32 inputs) in the layout [piece][step][kq][Mpad][8], gathering through kmap
+//             (act-order) on the way; rows M..Mpad are zero.
+//   k_gemm    128 x BN output tile per workgroup of 4 waves (2 x 2, each 64 x BN/2).  Per K
+//             chunk the workgroup copies the A operands of its 128 rows to LDS (double-buffered,
+//             the next chunk's global loads in flight during the current chunk's MFMAs), while
+//             every wave loads its own weight codes straight into registers (one 128-bit load
+//             per lane per 16-column tile), unpacks them into exact f16 (q - z) and runs
+//             v_mfma_f32_16x16x32_f16.  Group scales are applied in fp32 once per chunk; MXFP4
+//             block scales are folded into the fp4 -> f16 conversion relative to a per-column
+//             exponent (exact for every block within 2^23 of the column's largest), which is
+//             applied at the end.
+#include "sglq_dev.hpp"
+
+namespace {
+
+constexpr int BM = 128;
+
+__device__ __forceinline__ float act_at(const void *A, int dt, int64_t i) {
+  if (dt == SGLQ_DT_F32) return ((const float *)A)[i];
+  const uint32_t b = ((const uint16_t *)A)[i];
+  if (dt == SGLQ_DT_BF16) return __uint_as_float(b << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
+}
+
+__device__ __forceinline__ constexpr int kofs4(int i) { return (i >> 1) + 4 * (i & 1); }
+
+// One workgroup (256 threads) per row of Aop (Mpad rows).
+__global__ __launch_bounds__(256) void k_prep_a(const void *__restrict__ A, int dt, int64_t lda,
+                                                int M, int Mpad, int K, int nsteps,
+                                                const int32_t *__restrict__ kmap, int perm4,
+                                                int split, half8_t *__restrict__ aop,
+                                                int *__restrict__ rowexp) {
+  const int m = blockIdx.x;
+  const int tid = threadIdx.x;
+  __shared__ float red[4];
+  const int kp_n = nsteps * 32;
+  const int64_t plane = (int64_t)nsteps * 4 * Mpad;  // 16-B items per piece
+  if (m >= M) {
+    const half8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int it = tid; it < nsteps * 4; it += 256) {
+      aop[(int64_t)it * Mpad + m] = z;
+      if (split) aop[plane + (int64_t)it * Mpad + m] = z;
+    }
+    if (tid == 0) rowexp[m] = 0;
+    return;
+  }
+  const int64_t rb = (int64_t)m * lda;
+  float mx = 0.f;
+  for (int kp = tid; kp < kp_n; kp += 256) {
+    const int k = kmap ? kmap[kp] : (kp < K ? kp : -1);
+    if (k >= 0) mx = fmaxf(mx, fabsf(act_at(A, dt, rb + k)));
+  }
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const int e = (mx > 0.f && mx <= 3.0e38f) ? ilogbf(mx) - 13 : 0;
+  if (tid == 0) rowexp[m] = e;
+  for (int it = tid; it < nsteps * 4; it += 256) {  // it = step * 4 + kq
+    half8_t hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int kp = it * 8 + (perm4 ? kofs4(i) : i);
+      const int k = kmap ? kmap[kp] : (kp < K ? kp : -1);
+      const float x = k >= 0 ? ldexpf(act_at(A, dt, rb + k), -e) : 0.f;
+      const _Float16 h = (_Float16)x;
+      hi[i] = h;
+      lo[i] = (_Float16)(x - (float)h);
+    }
+    aop[(int64_t)it * Mpad + m] = hi;
+    if (split) aop[plane + (int64_t)it * Mpad + m] = lo;
+  }
+}
+
+struct GemmArgs {
+  const u32x4_t *codes;
+  const void *meta;
+  const uint8_t *colexp;  // E2M1: per-column reference exponent (largest e8m0 of the column)
+  const half8_t *aop;    // [np][nsteps][4][Mpad]
+  const int *rowexp;
+  const float *bias;
+  float *C;
+  int64_t ldc;
+  int M, Mpad, N, ntile, nchunk, nsteps, nmeta, cpg, nbn;
+};
+
+union H8 {
+  half8_t v;
+  uint32_t u[4];
+  half2_t h[4];
+};
+
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(o));
+  return r;
+}
+
+template <int KIND>
+__device__ __forceinline__ half8_t unpack_b(const u32x4_t &w, int j, half2_t zA, half2_t zB,
+                                            float fsc) {
+  H8 r;
+  if constexpr (KIND == SGLQ_KIND_U4) {
+    const uint32_t x = w[j], y = x >> 8;
+    r.u[0] = and_or(x, 0x000F000Fu, 0x64006400u);
+    r.u[1] = and_or(x, 0x00F000F0u, 0x54005400u);
+    r.u[2] = and_or(y, 0x000F000Fu, 0x64006400u);
+    r.u[3] = and_or(y, 0x00F000F0u, 0x54005400u);
+    r.h[0] = r.h[0] + zA;
+    r.h[1] = r.h[1] + zB;
+    r.h[2] = r.h[2] + zA;
+    r.h[3] = r.h[3] + zB;
+  } else if constexpr (KIND == SGLQ_KIND_U8) {
+    const uint32_t x0 = w[2 * j], x1 = w[2 * j + 1];
+    r.u[0] = __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u);
+    r.u[1] = __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u);
+    r.u[2] = __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u);
+    r.u[3] = __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u);
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.h[i] = r.h[i] + zA;
+  } else {
+    const uint32_t x = w[j];
+    r.h[0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(x, fsc, 0);
+    r.h[1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(x, fsc, 1);
+    r.h[2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(x, fsc, 2);
+    r.h[3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(x, fsc, 3);
+  }
+  return r.v;
+}
+
+template <bool SCF16>
+using meta_t = typename std::conditional<SCF16, uint32_t, uint64_t>::type;
+
+template <bool SCF16>
+__device__ __forceinline__ void decode_meta(meta_t<SCF16> m, float &sc, half2_t &zA,
+                                            half2_t &zB) {
+  uint32_t zb;
+  if constexpr (SCF16) {
+    sc = (float)__builtin_bit_cast(_Float16, (uint16_t)(m & 0xFFFFu));
+    zb = m >> 16;
+  } else {
+    sc = __uint_as_float((uint32_t)m);
+    zb = (uint32_t)(m >> 32) & 0xFFFFu;
+  }
+  const _Float16 z = __builtin_bit_cast(_Float16, (uint16_t)zb);
+  zA = (half2_t){z, z};
+  const _Float16 z2 = z + (_Float16)960.0f;
+  zB = (half2_t){z2, z2};
+}
+
+// 2^(e - ref) as f32 (0 for the reference's e == 255 "no scale" code and for underflow)
+__device__ __forceinline__ float e8m0_rel(uint32_t e, int ref) {
+  const int d = (int)e - ref + 127;
+  return (e == 255u || d <= 0) ? 0.f : __uint_as_float((uint32_t)d << 23);
+}
+
+template <int KIND, bool SPLIT, bool SCF16, bool STEPM, int BN>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
+  constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
+  constexpr int NP = SPLIT ? 2 : 1;
+  constexpr int TN = BN / 32;  // 16-column tiles per wave
+  constexpr int MB = 4;        // 16-row blocks per wave (64 rows)
+  constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
+  constexpr int ITEMS = NP * SPC * 4 * BM;  // 16-B A items per chunk
+  constexpr int IPT = ITEMS / 256;          // per thread
+  extern __shared__ half8_t s_a[];          // [2][NP][SPC][4][BM]
+
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int wm = w & 1, wn = w >> 1;
+  const int n16 = lane & 15, kq = lane >> 4;
+  const int bn = blockIdx.x % a.nbn, bm = blockIdx.x / a.nbn;
+  const int m0 = bm * BM;
+  const int64_t plane = (int64_t)a.nsteps * 4 * a.Mpad;
+
+  // A tile items of chunk c: item i -> (p, j, kq', row)
+  auto a_src = [&](int c, int i) -> const half8_t * {
+    const int row = i % BM, r = i / BM;  // r = (p * SPC + j) * 4 + kq'
+    const int p = r / (SPC * 4), sj = r % (SPC * 4);
+    return a.aop + p * plane + ((int64_t)(c * SPC) * 4 + sj) * a.Mpad + m0 + row;
+  };
+  half8_t areg[IPT];
+  auto load_a = [&](int c) {
+#pragma unroll
+    for (int q = 0; q < IPT; q++) areg[q] = *a_src(c, tid + 256 * q);
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < IPT; q++) s_a[buf * ITEMS + tid + 256 * q] = areg[q];
+  };
+
+  // weights of this wave: tiles t0 .. t0+TN-1
+  const int t0 = bn * (BN / 16) + wn * TN;
+  using MT = typename std::conditional<E2M1, uint32_t, meta_t<SCF16>>::type;
+  constexpr int NMV = STEPM ? SPC : 1;
+  u32x4_t bw[TN];
+  MT bm_[TN][NMV];
+  int cref[TN];
+  auto load_b = [&](int c, int g) {
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int t = min(t0 + j, a.ntile - 1);
+      bw[j] = __builtin_nontemporal_load(a.codes + ((int64_t)t * a.nchunk + c) * 64 + lane);
+      const int64_t mrow = ((int64_t)t * 16 + n16) * a.nmeta;
+      if constexpr (E2M1) {
+        bm_[j][0] = ((const uint32_t *)((const uint8_t *)a.meta + mrow))[c];
+      } else if constexpr (STEPM) {
+#pragma unroll
+        for (int s = 0; s < SPC; s++) bm_[j][s] = ((const MT *)a.meta)[mrow + c * SPC + s];
+      } else {
+        bm_[j][0] = ((const MT *)a.meta)[mrow + g];
+      }
+    }
+  };
+  if constexpr (E2M1) {
+#pragma unroll
+    for (int j = 0; j < TN; j++) cref[j] = a.colexp[min(t0 + j, a.ntile - 1) * 16 + n16];
+  }
+
+  float4_t acc[MB][TN], tmp[MB][TN];
+#pragma unroll
+  for (int i = 0; i < MB; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      acc[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      tmp[i][j] = acc[i][j];
+    }
+
+  int g = 0, gr = 0;  // group of the current chunk (META_GROUP), chunks into it
+  load_a(0);
+  load_b(0, 0);
+  store_a(0);
+  __syncthreads();
+  for (int c = 0; c < a.nchunk; c++) {
+    const int buf = c & 1;
+    u32x4_t cw[TN];
+    MT cm[TN][NMV];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      cw[j] = bw[j];
+#pragma unroll
+      for (int s = 0; s < NMV; s++) cm[j][s] = bm_[j][s];
+    }
+    if (++gr == a.cpg) {
+      gr = 0;
+      g++;
+    }
+    if (c + 1 < a.nchunk) {
+      load_a(c + 1);
+      load_b(c + 1, g);
+    }
+    // compute chunk c from LDS buffer buf and registers cw / cm
+    const half8_t *sa = s_a + buf * ITEMS + wm * 64 + n16;
+    float sc[TN];
+    half2_t zA[TN], zB[TN];
+    if constexpr (!E2M1 && !STEPM) {
+#pragma unroll
+      for (int j = 0; j < TN; j++) decode_meta<SCF16>(cm[j][0], sc[j], zA[j], zB[j]);
+    }
+#pragma unroll
+    for (int s = 0; s < SPC; s++) {
+      half8_t av[NP][MB];
+#pragma unroll
+      for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int i = 0; i < MB; i++) av[p][i] = sa[((p * SPC + s) * 4 + kq) * BM + i * 16];
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        float fsc = 1.f;
+        if constexpr (STEPM) decode_meta<SCF16>(cm[j][s], sc[j], zA[j], zB[j]);
+        if constexpr (E2M1) fsc = e8m0_rel((cm[j][0] >> (8 * s)) & 255u, cref[j]);
+        const half8_t b = unpack_b<KIND>(cw[j], s, zA[j], zB[j], fsc);
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+#pragma unroll
+          for (int p = 0; p < NP; p++)
+            tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[p][i], b, tmp[i][j], 0, 0, 0);
+        }
+        if constexpr (STEPM) {
+#pragma unroll
+          for (int i = 0; i < MB; i++) {
+            acc[i][j] += sc[j] * tmp[i][j];
+            tmp[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+          }
+        }
+      }
+    }
+    if constexpr (!STEPM && !E2M1) {
+#pragma unroll
+      for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          acc[i][j] += sc[j] * tmp[i][j];
+          tmp[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    if (c + 1 < a.nchunk) {
+      store_a(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // epilogue: lane holds rows 4*kq + r of each 16-row block, column n16 of each tile.  MXFP4
+  // sums stay in tmp (block scales were folded into the weights) and take the column exponent.
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const int n = (t0 + j) * 16 + n16;
+    if (n >= a.N) continue;
+    const float bv = a.bias ? a.bias[n] : 0.f;
+    const int ce = E2M1 ? cref[j] - 127 : 0;
+#pragma unroll
+    for (int i = 0; i < MB; i++) {
+      const float4_t r4 = E2M1 ? tmp[i][j] : acc[i][j];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int m = m0 + wm * 64 + i * 16 + 4 * kq + r;
+        if (m < a.M) a.C[(int64_t)m * a.ldc + n] = ldexpf(r4[r], a.rowexp[m] + ce) + bv;
+      }
+    }
+  }
+}
+
+template <int KIND, bool SPLIT, bool SCF16, bool STEPM>
+void launch_bn(const GemmArgs &a, int bn, unsigned grid, size_t lds, hipStream_t st) {
+  // LDS beyond 64 KiB must be enabled per kernel once (160 KiB on gfx950)
+  static bool raised128 = false, raised64 = false;
+  if (bn == 128) {
+    auto f = k_gemm<KIND, SPLIT, SCF16, STEPM, 128>;
+    if (!raised128)
+      raised128 = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      160 * 1024) == hipSuccess;
+    f<<<grid, 256, lds, st>>>(a);
+  } else {
+    auto f = k_gemm<KIND, SPLIT, SCF16, STEPM, 64>;
+    if (!raised64)
+      raised64 = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     160 * 1024) == hipSuccess;
+    f<<<grid, 256, lds, st>>>(a);
+  }
+}
+
+template <int KIND, bool SPLIT>
+void launch_meta(const GemmArgs &a, int scf16, int stepm, int bn, unsigned grid, size_t lds,
+                 hipStream_t st) {
+  if constexpr (KIND == SGLQ_KIND_E2M1) {
+    launch_bn<KIND, SPLIT, true, false>(a, bn, grid, lds, st);
+  } else {
+    if (scf16) {
+      if (stepm)
+        launch_bn<KIND, SPLIT, true, true>(a, bn, grid, lds, st);
+      else
+        launch_bn<KIND, SPLIT, true, false>(a, bn, grid, lds, st);
+    } else {
+      if (stepm)
+        launch_bn<KIND, SPLIT, false, true>(a, bn, grid, lds, st);
+      else
+        launch_bn<KIND, SPLIT, false, false>(a, bn, grid, lds, st);
+    }
+  }
+}
+
+template <int KIND>
+void launch_split(const GemmArgs &a, bool split, int scf16, int stepm, int bn, unsigned grid,
+                  size_t lds, hipStream_t st) {
+  if (split)
+    launch_meta<KIND, true>(a, scf16, stepm, bn, grid, lds, st);
+  else
+    launch_meta<KIND, false>(a, scf16, stepm, bn, grid, lds, st);
+}
+
+}  // namespace
+
+int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
+              float *C, int64_t ldc, hipStream_t st) {
+  const bool split = dt == SGLQ_DT_F32;
+  const int np = split ? 2 : 1;
+  const int64_t Mpad = (M + BM - 1) / BM * BM;
+  const size_t aop_bytes = (size_t)np * d->nsteps * 4 * Mpad * 16;
+  const size_t need = aop_bytes + (size_t)Mpad * sizeof(int) + 256;
+  if (sglq_ws_reserve(d, need) != 0) return -1;
+  half8_t *aop = (half8_t *)d->ws;
+  int *rowexp = (int *)((char *)d->ws + aop_bytes);
+  k_prep_a<<<(unsigned)Mpad, 256, 0, st>>>(A, dt, lda, (int)M, (int)Mpad, (int)d->K,
+                                           (int)d->nsteps, d->kident ? nullptr : d->kmap,
+                                           d->kind == SGLQ_KIND_U4, split, aop, rowexp);
+  SGLQ_HIP(hipGetLastError());
+  {
+    // 128-column tiles unless that leaves the chip under-filled
+    const int64_t nbm = Mpad / BM;
+    int bn = 128;
+    if (nbm * ((d->N + 127) / 128) < 512 || d->meta_mode == SGLQ_META_STEP) bn = 64;
+    const int nbn = (int)((d->N + bn - 1) / bn);
+    const int spc = (int)d->spc;
+    const size_t lds = (size_t)2 * np * spc * 4 * BM * 16;
+    GemmArgs a;
+    a.codes = d->codes;
+    a.meta = d->meta;
+    a.colexp = d->colexp;
+    a.aop = aop;
+    a.rowexp = rowexp;
+    a.bias = bias;
+    a.C = C;
+    a.ldc = ldc;
+    a.M = (int)M;
+    a.Mpad = (int)Mpad;
+    a.N = (int)d->N;
+    a.ntile = (int)d->ntile;
+    a.nchunk = (int)d->nchunk;
+    a.nsteps = (int)d->nsteps;
+    a.nmeta = (int)d->nmeta;
+    a.cpg = d->cpg > 0 ? (int)d->cpg : 1;
+    a.nbn = nbn;
+    const unsigned grid = (unsigned)(nbm * nbn);
+    const int stepm = d->meta_mode == SGLQ_META_STEP;
+    switch (d->kind) {
+      case SGLQ_KIND_U4:
+        launch_split<SGLQ_KIND_U4>(a, split, d->scf16, stepm, bn, grid, lds, st);
+        break;
+      case SGLQ_KIND_U8:
+        launch_split<SGLQ_KIND_U8>(a, split, d->scf16, stepm, bn, grid, lds, st);
+        break;
+      default:
+        launch_split<SGLQ_KIND_E2M1>(a, split, 1, 0, bn, grid, lds, st);
+        break;
+    }
+    SGLQ_HIP(hipGetLastError());
+  }
+  return 0;
+fail:
+  return -1;
+}

@@ -1,28 +1,27 @@
 // gemv.hip — decode-side quantized linear, C[M,N] = A[M,K] * W^T (+ bias) for M <= 16.
 //
-// Work split: a workgroup is 4 waves; wave w owns the 16-column tile t = 4*cg + w, and all four
-// waves walk the same K range (CPW chunks), so the activations of that range are staged once
-// per workgroup in LDS.  The grid is (column groups) x (K ranges); K ranges of one column group
-// leave fp32 partial sums in a per-handle buffer and the last workgroup to arrive (an arrival
-// counter per column group) adds them in K order and writes C.  No atomics touch C, so the
-// result is deterministic, and every counter is back at zero when a launch ends.
+// Work split: a workgroup stages one K range of the activations in LDS and its ks x tpg waves
+// split that range into ks slices of CPW chunks over tpg 16-column tiles; the slices of a tile
+// are added through LDS in slice order.  When K is longer than one workgroup's range (large M
+// shrinks the staging budget), the ranges of one column group leave fp32 partial sums in a
+// per-handle buffer and the last workgroup to arrive (an arrival counter) adds them in K order.
+// No atomics touch C, so the result is deterministic, and every counter is back at zero when a
+// launch ends.
 //
 // Weight codes are streamed once with one 128-bit non-temporal load per lane per chunk, all
-// of a wave's chunks issued before any is consumed.  Codes are unpacked in registers straight
-// into the B operand of v_mfma_f32_16x16x32_f16 with the zero subtracted exactly in f16
-// (q - z is a small integer), so the fp32 MFMA accumulation sees exact weight codes.  The
-// group scale is applied in fp32 per chunk (per step for MXFP4's e8m0 block scales and for
-// group sizes that are not whole chunks).
+// of a wave's chunks issued before any is consumed and before the activation staging.  Codes
+// are unpacked in registers straight into the B operand of v_mfma_f32_16x16x32_f16 with the
+// zero subtracted exactly in f16 (q - z is a small integer), so the fp32 MFMA accumulation sees
+// exact weight codes.  The group scale is applied in fp32 per chunk (per step for MXFP4's e8m0
+// block scales and for group sizes that are not whole chunks).
 //
 // Activations: each workgroup finds, per row, the largest |a| over its K range and scales the
 // row by an exact power of two so it sits well inside f16 range; f32 inputs are split into f16
 // hi + lo parts (about 22 significant bits), bf16/f16 inputs fit one f16 part.  The power of
-// two is undone exactly on the partial sum.
+// two is undone exactly on the result.
 #include "sglq_dev.hpp"
 
 namespace {
-
-constexpr int kWaves = 4;
 
 struct GemvArgs {
   const u32x4_t *codes;
@@ -34,7 +33,7 @@ struct GemvArgs {
   float *part;  // [S][M][N]
   int *cnt;     // [ncg]
   int64_t lda, ldc;
-  int N, K, M, adt, ntile, nchunk, nmeta, cpg, S, ncg;
+  int N, K, M, adt, ntile, nchunk, nmeta, cpg, S, ncg, ks, tpg;
 };
 
 __device__ __forceinline__ float bf16_bits(uint32_t b) { return __uint_as_float(b << 16); }
@@ -135,44 +134,48 @@ __device__ __forceinline__ void decode_meta(meta_t<SCF16> m, float &sc, half2_t 
 __device__ __forceinline__ constexpr int kofs4(int i) { return (i >> 1) + 4 * (i & 1); }
 
 template <int KIND, int CPW, bool SPLIT, bool SCF16, bool STEPM, bool FAST>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+__global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
-  constexpr int SL = CPW * SPC;  // steps in one K range
-  constexpr int IPR = SL * 4;    // 8-element activation items per row
   constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
-  constexpr int RS = IPR + 1;    // LDS row stride in 16-B items (+1 spreads rows over banks)
-  extern __shared__ half8_t s_act[];  // [SPLIT ? 2 : 1][M][RS]
+  constexpr int NP = SPLIT ? 2 : 1;
+  constexpr int RW = SPLIT ? 2 : 1;  // 128-bit words per 8-element activation item
+  constexpr int KEEP = 4;            // items per thread held in registers across the passes
+  extern __shared__ half8_t s_act[];  // [NP][M][RS] activation operands, then [waves][64] acc
   __shared__ unsigned s_amax[16];
   __shared__ int s_exp[16];
   __shared__ int s_last;
 
+  const int nthr = blockDim.x;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int cg = (int)(blockIdx.x % (unsigned)a.ncg), sidx = (int)(blockIdx.x / (unsigned)a.ncg);
-  const int c0 = sidx * CPW;
-  const int nc = min(CPW, a.nchunk - c0);
-  const int kp0 = c0 * SPC * 32;
+  const int tt = w / a.ks, ks = w - tt * a.ks;     // tile within the group, K slice
+  const int cw0 = sidx * a.ks * CPW;              // first chunk of the workgroup's K range
+  const int c0 = cw0 + ks * CPW;                  // first chunk of this wave
+  const int ncw = min(a.ks * CPW, a.nchunk - cw0);  // chunks in the workgroup's range
+  const int kp0 = cw0 * SPC * 32;
   const int M = a.M;
+  const int IPR = a.ks * CPW * SPC * 4;           // 8-element activation items per row
+  const int RS = IPR + 1;                         // LDS row stride (+1 spreads rows over banks)
   const int items = M * IPR;
-  const int t = cg * kWaves + w;
+  const int t = cg * a.tpg + tt;
   const bool tvalid = t < a.ntile;
   const int tl = min(t, a.ntile - 1);  // waves past the last tile load valid memory, unused
   const int n16 = lane & 15, kq = lane >> 4;
 
-  // ---- activations of this K range: the first two 8-element items of every thread are
-  // loaded before the weight loads (vmcnt retires in order, so they can be consumed while the
-  // weights are still in flight) and stay in registers until they are converted
+  // ---- activation items: the first KEEP per thread are loaded before the weight loads
+  // (vmcnt retires in order, so they can be consumed while the weights are still in flight).
+  // FAST items are one (16-bit) or two (f32) 128-bit loads from a clamped, always-valid
+  // address with no branch; decoding to f32 happens at first use.
   if (tid < 16) s_amax[tid] = 0u;
-  // raw 8-element items: FAST loads are one (16-bit) or two (f32) 128-bit loads from a clamped,
-  // always-valid address with no branch; decoding to f32 happens at first use
-  constexpr int RW = SPLIT ? 2 : 1;
   struct Raw {
     u32x4_t q[RW];
     bool ok;
   };
+  auto item_kp = [&](int r) { return kp0 + (r >> 2) * 32 + (r & 3) * 8; };
   auto load_raw = [&](int it, Raw &x) {
-    const int m = it / IPR, r = it % IPR;
-    const int kp = kp0 + (r >> 2) * 32 + (r & 3) * 8;
-    x.ok = (r >> 2) < nc * SPC && it < items && (!FAST || kp < a.K);
+    const int m = it / IPR, r = it - m * IPR;
+    const int kp = item_kp(r);
+    x.ok = it < items && (r >> 2) < ncw * SPC && (!FAST || kp < a.K);
     if constexpr (FAST) {
       const int64_t off = (int64_t)min(m, M - 1) * a.lda + (x.ok ? kp : 0);
       const u32x4_t *p = (const u32x4_t *)((const char *)a.A + off * (SPLIT ? 4 : 2));
@@ -196,14 +199,9 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
         for (int o = 0; o < 8; o++) v[o] = f16_bits((x.q[0][o >> 1] >> (16 * (o & 1))) & 0xFFFFu);
       }
     } else {
-      const int m = it / IPR, r = it % IPR;
-      load8(a, m, kp0 + (r >> 2) * 32 + (r & 3) * 8, v);
+      const int m = it / IPR;
+      load8(a, m, item_kp(it - m * IPR), v);
     }
-  };
-  auto load_item = [&](int it, float (&v)[8]) {
-    Raw x;
-    load_raw(it, x);
-    decode_raw(it, x, v);
   };
   auto amax_item = [&](int it, const float (&v)[8]) {
     float mx = 0.f;
@@ -212,7 +210,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     atomicMax(&s_amax[it / IPR], __float_as_uint(mx));
   };
   auto store_item = [&](int it, const float (&v)[8]) {
-    const int m = it / IPR, r = it % IPR;
+    const int m = it / IPR, r = it - m * IPR;
     const int e = s_exp[m];
     half8_t hi, lo;
 #pragma unroll
@@ -225,29 +223,32 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     s_act[m * RS + r] = hi;
     if constexpr (SPLIT) s_act[(M + m) * RS + r] = lo;
   };
-  Raw keep[2];
+  Raw keep[KEEP];
 #pragma unroll
-  for (int j = 0; j < 2; j++) load_raw(tid + 256 * j, keep[j]);
+  for (int j = 0; j < KEEP; j++) load_raw(tid + nthr * j, keep[j]);
 
   // ---- this wave's weight loads (meta, then codes), all issued before the activation
-  // staging so their HBM latency overlaps it.  Indices past the range are clamped to its last chunk (valid
-  // memory, never used), so the loads are straight-line code.
+  // staging so their HBM latency overlaps it.  Chunk indices are clamped into [0, nchunk)
+  // (valid memory; chunks past the wave's range are never accumulated), so the loads are
+  // straight-line code.
+  const int clast = a.nchunk - 1;
   constexpr int NMV = E2M1 ? CPW : (STEPM ? CPW * SPC : CPW);
   using MT = typename std::conditional<E2M1, uint32_t, meta_t<SCF16>>::type;
   MT mv[NMV];
   const int64_t mrow = ((int64_t)tl * 16 + n16) * a.nmeta;
   if constexpr (E2M1) {
-    const uint32_t *ep = (const uint32_t *)((const uint8_t *)a.meta + mrow) + c0;
+    const uint32_t *ep = (const uint32_t *)((const uint8_t *)a.meta + mrow);
 #pragma unroll
-    for (int i = 0; i < CPW; i++) mv[i] = ep[min(i, nc - 1)];
+    for (int i = 0; i < CPW; i++) mv[i] = ep[min(c0 + i, clast)];
   } else if constexpr (STEPM) {
-    const MT *mp = (const MT *)a.meta + mrow + (int64_t)c0 * SPC;
+    const MT *mp = (const MT *)a.meta + mrow;
 #pragma unroll
-    for (int i = 0; i < CPW * SPC; i++) mv[i] = mp[min(i, nc * SPC - 1)];
+    for (int i = 0; i < CPW * SPC; i++) mv[i] = mp[min(c0 * SPC + i, clast * SPC + SPC - 1)];
   } else {
     const MT *mp = (const MT *)a.meta + mrow;
-    int g = c0 / a.cpg, r = c0 - g * a.cpg;
-    const int glast = (c0 + nc - 1) / a.cpg;
+    const int cc = min(c0, clast);
+    int g = cc / a.cpg, r = cc - g * a.cpg;
+    const int glast = clast / a.cpg;
 #pragma unroll
     for (int i = 0; i < CPW; i++) {
       mv[i] = mp[min(g, glast)];
@@ -257,22 +258,25 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
       }
     }
   }
-  const u32x4_t *cp = a.codes + ((int64_t)tl * a.nchunk + c0) * 64 + lane;
+  const u32x4_t *cp = a.codes + (int64_t)tl * a.nchunk * 64 + lane;
   u32x4_t wv[CPW];
 #pragma unroll
-  for (int i = 0; i < CPW; i++) wv[i] = __builtin_nontemporal_load(cp + min(i, nc - 1) * 64);
+  for (int i = 0; i < CPW; i++) wv[i] = __builtin_nontemporal_load(cp + min(c0 + i, clast) * 64);
   __builtin_amdgcn_sched_barrier(0);  // keep the whole batch of loads ahead of the staging
 
+  // ---- stage the activations: per-row max |a| -> exact power-of-two scale -> f16 operands
   __syncthreads();  // s_amax cleared
-  float kv[2][8];
+  float kv[KEEP][8];
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    decode_raw(tid + 256 * j, keep[j], kv[j]);
-    if (tid + 256 * j < items) amax_item(tid + 256 * j, kv[j]);
+  for (int j = 0; j < KEEP; j++) {
+    decode_raw(tid + nthr * j, keep[j], kv[j]);
+    if (tid + nthr * j < items) amax_item(tid + nthr * j, kv[j]);
   }
-  for (int it = tid + 512; it < items; it += 256) {
+  for (int it = tid + nthr * KEEP; it < items; it += nthr) {
+    Raw x;
     float v[8];
-    load_item(it, v);
+    load_raw(it, x);
+    decode_raw(it, x, v);
     amax_item(it, v);
   }
   __syncthreads();
@@ -282,179 +286,238 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   }
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < 2; j++)
-    if (tid + 256 * j < items) store_item(tid + 256 * j, kv[j]);
-  for (int it = tid + 512; it < items; it += 256) {
+  for (int j = 0; j < KEEP; j++)
+    if (tid + nthr * j < items) store_item(tid + nthr * j, kv[j]);
+  for (int it = tid + nthr * KEEP; it < items; it += nthr) {
+    Raw x;
     float v[8];
-    load_item(it, v);
+    load_raw(it, x);
+    decode_raw(it, x, v);
     store_item(it, v);
   }
   __syncthreads();
 
-  // ---- multiply
+  // ---- multiply: chunks past the wave's range (c0 + i >= nchunk) run on zero activations
+  // with a zero scale, which keeps the code straight-line and every load ahead of its use.
+  // Lanes of rows >= M read row M-1 instead: an A row only feeds the same row of the
+  // product, and rows >= M are never written.
+  const half8_t *arow_p = s_act + min(n16, M - 1) * RS + ks * CPW * SPC * 4 + kq;
+  auto read_ops = [&](int i, half8_t (&op)[SPC * NP]) {
+#pragma unroll
+    for (int j = 0; j < SPC; j++) {
+      op[j] = arow_p[(i * SPC + j) * 4];
+      if constexpr (SPLIT) op[SPC + j] = arow_p[M * RS + (i * SPC + j) * 4];
+    }
+  };
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
-  {
-    // activation operands of one chunk.  Lanes of rows >= M read row M-1 instead: an A row
-    // only feeds the same row of the product, and rows >= M are never written.
-    constexpr int NP = SPLIT ? 2 : 1;
-    const half8_t *arow_p = s_act + min(n16, M - 1) * RS + kq;
-    auto read_ops = [&](int i, half8_t (&op)[SPC * NP]) {
+  float4_t t0 = {0.f, 0.f, 0.f, 0.f};
+  half8_t opc[SPC * NP], opn[SPC * NP];
+  read_ops(0, opc);
 #pragma unroll
-      for (int j = 0; j < SPC; j++) {
-        op[j] = arow_p[(i * SPC + j) * 4];
-        if constexpr (SPLIT) op[SPC + j] = arow_p[M * RS + (i * SPC + j) * 4];
-      }
-    };
-
-    float4_t t0 = {0.f, 0.f, 0.f, 0.f};
-    half8_t opc[SPC * NP], opn[SPC * NP];
-    read_ops(0, opc);
+  for (int i = 0; i < CPW; i++) {
+    const bool live = c0 + i < a.nchunk;
+    if (i + 1 < CPW) read_ops(i + 1, opn);
+    float sc = 0.f;
+    half2_t zA = {0, 0}, zB = {0, 0};
+    if constexpr (!E2M1 && !STEPM) {
+      decode_meta<SCF16>(mv[i], sc, zA, zB);
+      sc = live ? sc : 0.f;
+    }
 #pragma unroll
-    for (int i = 0; i < CPW; i++) {
-      // chunks past the range (i >= nc) run on zero activations with a zero scale: straight-
-      // line code keeps every load ahead of the arithmetic
-      const bool live = i < nc;
-      if (i + 1 < CPW) read_ops(i + 1, opn);
-      float sc = 0.f;
-      half2_t zA = {0, 0}, zB = {0, 0};
-      if constexpr (!E2M1 && !STEPM) {
-        decode_meta<SCF16>(mv[i], sc, zA, zB);
+    for (int j = 0; j < SPC; j++) {
+      if constexpr (!E2M1 && STEPM) {
+        decode_meta<SCF16>(mv[i * SPC + j], sc, zA, zB);
         sc = live ? sc : 0.f;
       }
-#pragma unroll
-      for (int j = 0; j < SPC; j++) {
-        if constexpr (!E2M1 && STEPM) {
-          decode_meta<SCF16>(mv[i * SPC + j], sc, zA, zB);
-          sc = live ? sc : 0.f;
+      const half8_t b = unpack<KIND>(wv[i], j, zA, zB);
+      t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[j], b, t0, 0, 0, 0);
+      if constexpr (SPLIT)
+        t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[SPC + j], b, t0, 0, 0, 0);
+      if constexpr (E2M1 || STEPM) {
+        if constexpr (E2M1) {
+          const uint32_t ex = (mv[i] >> (8 * j)) & 255u;
+          sc = (ex == 255u || !live) ? 0.f : ldexpf(1.0f, (int)ex - 127);  // ref qweight.c:361
         }
-        const half8_t b = unpack<KIND>(wv[i], j, zA, zB);
-        t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[j], b, t0, 0, 0, 0);
-        if constexpr (SPLIT)
-          t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[SPC + j], b, t0, 0, 0, 0);
-        if constexpr (E2M1 || STEPM) {
-          if constexpr (E2M1) {
-            const uint32_t ex = (mv[i] >> (8 * j)) & 255u;
-            sc = (ex == 255u || !live) ? 0.f : ldexpf(1.0f, (int)ex - 127);  // ref qweight.c:361
-          }
-          acc += sc * t0;
-          t0 = (float4_t){0.f, 0.f, 0.f, 0.f};
-        }
-      }
-      if constexpr (!E2M1 && !STEPM) {
         acc += sc * t0;
         t0 = (float4_t){0.f, 0.f, 0.f, 0.f};
       }
-#pragma unroll
-      for (int q = 0; q < SPC * NP; q++) opc[q] = opn[q];
     }
-
-    // lane holds rows 4*kq + i of column n (v_mfma_f32_16x16x32 C layout)
-    const int n = t * 16 + n16;
-    if (tvalid && n < a.N) {
+    if constexpr (!E2M1 && !STEPM) {
+      acc += sc * t0;
+      t0 = (float4_t){0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int r = 4 * kq + i;
-        if (r < M) {
-          const float v = ldexpf(acc[i], s_exp[r]);
-          if (a.S == 1)
-            a.C[r * a.ldc + n] = v + (a.bias ? a.bias[n] : 0.f);
-          else  // device-scope store: written through to the level all XCDs share
-            __hip_atomic_store(&a.part[((int64_t)sidx * M + r) * a.N + n], v, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        }
+    for (int q = 0; q < SPC * NP; q++) opc[q] = opn[q];
+  }
+
+  // ---- K slices of one tile are added in slice order through LDS (reusing the staging area)
+  if (a.ks > 1) {
+    float4_t *red = (float4_t *)s_act;
+    __syncthreads();  // every wave is done reading activations
+    red[w * 64 + lane] = acc;
+    __syncthreads();
+    if (ks != 0) return;
+    acc = red[w * 64 + lane];
+    for (int q = 1; q < a.ks; q++) acc += red[(w + q) * 64 + lane];
+  }
+
+  // lane holds rows 4*kq + i of column n (v_mfma_f32_16x16x32 C layout)
+  const int n = t * 16 + n16;
+  if (tvalid && n < a.N) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int r = 4 * kq + i;
+      if (r < M) {
+        const float v = ldexpf(acc[i], s_exp[r]);
+        if (a.S == 1)
+          a.C[r * a.ldc + n] = v + (a.bias ? a.bias[n] : 0.f);
+        else  // device-scope store: written through to the level all XCDs share
+          __hip_atomic_store(&a.part[((int64_t)sidx * M + r) * a.N + n], v, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
   if (a.S == 1) return;
 
-  // ---- split-K: the last workgroup of this column group adds the partials in K order.
-  // The partials are device-scope stores/loads, so no cache write-back or invalidate is
+  // ---- split-K over workgroups: the last workgroup of this column group adds the partials in
+  // K order.  Partials are device-scope stores/loads, so no cache write-back or invalidate is
   // needed; waiting for the stores' acknowledgement before the arrival increment orders them.
+  // (Only the ks == 0 waves are still running here.)
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  if (a.ks > 1) {
+    // the ks != 0 waves have left, so no workgroup barrier is possible: arrivals are counted
+    // per tile, by its ks == 0 wave
+    if (!tvalid) return;
+    int last = 0;
+    if (lane == 0)
+      last = __hip_atomic_fetch_add(&a.cnt[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             a.S - 1;
+    last = __shfl(last, 0);
+    if (!last) return;
+    for (int idx = lane; idx < M * 16; idx += 64) {
+      const int r = idx >> 4, nn = t * 16 + (idx & 15);
+      if (tvalid && nn < a.N) {
+        float sum = 0.f;
+        for (int s = 0; s < a.S; s++)
+          sum += __hip_atomic_load(&a.part[((int64_t)s * M + r) * a.N + nn], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        a.C[r * a.ldc + nn] = sum + (a.bias ? a.bias[nn] : 0.f);
+      }
+    }
+    if (lane == 0) __hip_atomic_store(&a.cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   __syncthreads();
   if (tid == 0)
     s_last = __hip_atomic_fetch_add(&a.cnt[cg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
              a.S - 1;
   __syncthreads();
   if (!s_last) return;
-  constexpr int NCOL = kWaves * 16;
-  for (int idx = tid; idx < M * NCOL; idx += 256) {
-    const int r = idx / NCOL, n = cg * NCOL + idx % NCOL;
-    if (n < a.N) {
+  const int ncol = a.tpg * 16;
+  for (int idx = tid; idx < M * ncol; idx += nthr) {
+    const int r = idx / ncol, nn = cg * ncol + idx % ncol;
+    if (nn < a.N) {
       float sum = 0.f;
       for (int s = 0; s < a.S; s++)
-        sum += __hip_atomic_load(&a.part[((int64_t)s * M + r) * a.N + n], __ATOMIC_RELAXED,
+        sum += __hip_atomic_load(&a.part[((int64_t)s * M + r) * a.N + nn], __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
-      a.C[r * a.ldc + n] = sum + (a.bias ? a.bias[n] : 0.f);
+      a.C[r * a.ldc + nn] = sum + (a.bias ? a.bias[nn] : 0.f);
     }
   }
   if (tid == 0) __hip_atomic_store(&a.cnt[cg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int KIND, int CPW, bool SPLIT, bool FAST>
-void launch4(const GemvArgs &a, int scf16, int stepm, size_t lds, unsigned grid,
+void launch4(const GemvArgs &a, int scf16, int stepm, size_t lds, unsigned grid, unsigned nthr,
              hipStream_t st) {
   if constexpr (KIND == SGLQ_KIND_E2M1) {
-    k_gemv<KIND, CPW, SPLIT, true, false, FAST><<<grid, 256, lds, st>>>(a);
+    k_gemv<KIND, CPW, SPLIT, true, false, FAST><<<grid, nthr, lds, st>>>(a);
   } else {
     if (scf16) {
       if (stepm)
-        k_gemv<KIND, CPW, SPLIT, true, true, FAST><<<grid, 256, lds, st>>>(a);
+        k_gemv<KIND, CPW, SPLIT, true, true, FAST><<<grid, nthr, lds, st>>>(a);
       else
-        k_gemv<KIND, CPW, SPLIT, true, false, FAST><<<grid, 256, lds, st>>>(a);
+        k_gemv<KIND, CPW, SPLIT, true, false, FAST><<<grid, nthr, lds, st>>>(a);
     } else {
       if (stepm)
-        k_gemv<KIND, CPW, SPLIT, false, true, FAST><<<grid, 256, lds, st>>>(a);
+        k_gemv<KIND, CPW, SPLIT, false, true, FAST><<<grid, nthr, lds, st>>>(a);
       else
-        k_gemv<KIND, CPW, SPLIT, false, false, FAST><<<grid, 256, lds, st>>>(a);
+        k_gemv<KIND, CPW, SPLIT, false, false, FAST><<<grid, nthr, lds, st>>>(a);
     }
   }
 }
 
-template <int KIND, int CPW, bool SPLIT>
-void launch3(const GemvArgs &a, int scf16, int stepm, bool fast, size_t lds, unsigned grid,
-             hipStream_t st) {
-  if (fast)
-    launch4<KIND, CPW, SPLIT, true>(a, scf16, stepm, lds, grid, st);
-  else
-    launch4<KIND, CPW, SPLIT, false>(a, scf16, stepm, lds, grid, st);
+template <int KIND, int CPW>
+void launch_cpw(const GemvArgs &a, bool split, int scf16, int stepm, bool fast, size_t lds,
+                unsigned grid, unsigned nthr, hipStream_t st) {
+  if (split) {
+    if (fast)
+      launch4<KIND, CPW, true, true>(a, scf16, stepm, lds, grid, nthr, st);
+    else
+      launch4<KIND, CPW, true, false>(a, scf16, stepm, lds, grid, nthr, st);
+  } else {
+    if (fast)
+      launch4<KIND, CPW, false, true>(a, scf16, stepm, lds, grid, nthr, st);
+    else
+      launch4<KIND, CPW, false, false>(a, scf16, stepm, lds, grid, nthr, st);
+  }
 }
 
 template <int KIND>
 void launch_kind(const GemvArgs &a, int cpw, bool split, int scf16, int stepm, bool fast,
-                 size_t lds, unsigned grid, hipStream_t st) {
-  if (cpw == 8) {
-    if (split)
-      launch3<KIND, 8, true>(a, scf16, stepm, fast, lds, grid, st);
-    else
-      launch3<KIND, 8, false>(a, scf16, stepm, fast, lds, grid, st);
-  } else {
-    if (split)
-      launch3<KIND, 4, true>(a, scf16, stepm, fast, lds, grid, st);
-    else
-      launch3<KIND, 4, false>(a, scf16, stepm, fast, lds, grid, st);
+                 size_t lds, unsigned grid, unsigned nthr, hipStream_t st) {
+  switch (cpw) {
+    case 4: launch_cpw<KIND, 4>(a, split, scf16, stepm, fast, lds, grid, nthr, st); break;
+    case 12: launch_cpw<KIND, 12>(a, split, scf16, stepm, fast, lds, grid, nthr, st); break;
+    default: launch_cpw<KIND, 8>(a, split, scf16, stepm, fast, lds, grid, nthr, st); break;
   }
 }
 
-constexpr size_t kMaxLds = 48 * 1024;
+constexpr size_t kLdsBudget = 60 * 1024;
+constexpr int kMaxWaves = 8;  // per workgroup (the kernel's launch bound is 512 threads)
 
-size_t act_lds(const sglq_dev *d, int cpw, bool split, int64_t M) {
-  return (size_t)(split ? 2 : 1) * (cpw * d->spc * 4 + 1) * M * 16;
+struct Plan {
+  int cpw, ks, tpg, S, ncg;
+  size_t lds;
+};
+
+// Work split for one launch.  A workgroup stages one K range of the activations in LDS and
+// its ks x tpg waves split that range (ks slices of cpw chunks) over tpg tiles; ranges beyond
+// one workgroup (K longer than the staging budget allows) are added across workgroups.
+Plan plan_gemv(const sglq_dev *d, int64_t M, bool split) {
+  const int64_t np = split ? 2 : 1;
+  const int64_t max_chunks = ((int64_t)kLdsBudget / (np * M * 16) - 1) / (d->spc * 4);
+  Plan best = {0, 0, 0, 1 << 30, 0, 0};
+  const int cand[3] = {8, 12, 4};
+  for (int cpw : cand) {
+    int64_t ks = (d->nchunk + cpw - 1) / cpw;
+    ks = ks < kMaxWaves ? ks : kMaxWaves;
+    const int64_t kl = max_chunks / cpw;
+    ks = ks < kl ? ks : kl;
+    if (ks < 1) continue;
+    const int S = (int)((d->nchunk + ks * cpw - 1) / (ks * cpw));
+    if (S < best.S) best = {cpw, (int)ks, 0, S, 0, 0};
+  }
+  if (best.cpw == 0) best = {4, 1, 0, (int)((d->nchunk + 3) / 4), 0, 0};
+  best.tpg = best.ks >= 4 ? 1 : 4 / best.ks;
+  best.ncg = (int)((d->ntile + best.tpg - 1) / best.tpg);
+  const size_t stage = (size_t)np * M * (best.ks * best.cpw * d->spc * 4 + 1) * 16;
+  const size_t red = (size_t)best.ks * best.tpg * 64 * 16;
+  best.lds = stage > red ? stage : red;
+  return best;
 }
 
 }  // namespace
 
 int sglq_gemv_setup(sglq_dev *d) {
-  const int64_t ncg = (d->ntile + kWaves - 1) / kWaves;
-  // 8 chunks (8 KiB of codes per wave) unless that leaves fewer than two workgroups per CU
-  d->gv_cpw = (ncg * ((d->nchunk + 7) / 8) < 512 && d->nchunk > 4) ? 4 : 8;
-  d->gv_split = (int)((d->nchunk + 3) / 4);  // the most K ranges any launch uses (cpw = 4)
+  // the most K ranges any launch splits over (cpw = 4, one slice per workgroup)
+  d->gv_split = (int)((d->nchunk + 3) / 4);
   if (d->gv_split > 1) {
     SGLQ_HIP(hipMalloc(&d->gv_part, (size_t)d->gv_split * 16 * d->N * sizeof(float)));
-    SGLQ_HIP(hipMalloc(&d->gv_cnt, (size_t)ncg * sizeof(int)));
-    SGLQ_HIP(hipMemset(d->gv_cnt, 0, (size_t)ncg * sizeof(int)));
+    SGLQ_HIP(hipMalloc(&d->gv_cnt, (size_t)d->ntile * sizeof(int)));
+    SGLQ_HIP(hipMemset(d->gv_cnt, 0, (size_t)d->ntile * sizeof(int)));
   }
   return 0;
 fail:
@@ -464,10 +527,7 @@ fail:
 int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
               float *C, int64_t ldc, hipStream_t st) {
   const bool split = dt == SGLQ_DT_F32;
-  int cpw = d->gv_cpw;
-  if (act_lds(d, cpw, split, M) > kMaxLds) cpw = 4;
-  const int S = (int)((d->nchunk + cpw - 1) / cpw);
-  const int ncg = (int)((d->ntile + kWaves - 1) / kWaves);
+  const Plan pl = plan_gemv(d, M, split);
   const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
   GemvArgs a;
   a.codes = d->codes;
@@ -488,17 +548,29 @@ int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
   a.nchunk = (int)d->nchunk;
   a.nmeta = (int)d->nmeta;
   a.cpg = d->cpg > 0 ? (int)d->cpg : 1;
-  a.S = S;
-  a.ncg = ncg;
+  a.S = pl.S;
+  a.ncg = pl.ncg;
+  a.ks = pl.ks;
+  a.tpg = pl.tpg;
   const bool fast = d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
                     (lda * esz) % 16 == 0;
-  const size_t lds = act_lds(d, cpw, split, M);
-  const unsigned grid = (unsigned)(ncg * S);
+  const unsigned grid = (unsigned)(pl.ncg * pl.S);
+  const unsigned nthr = (unsigned)(pl.ks * pl.tpg * 64);
   const int stepm = d->meta_mode == SGLQ_META_STEP;
+  if (pl.S > d->gv_split) {
+    sglq_log_error("qlinear: GEMV split %d exceeds its state (%d)", pl.S, d->gv_split);
+    return -1;
+  }
   switch (d->kind) {
-    case SGLQ_KIND_U4: launch_kind<SGLQ_KIND_U4>(a, cpw, split, d->scf16, stepm, fast, lds, grid, st); break;
-    case SGLQ_KIND_U8: launch_kind<SGLQ_KIND_U8>(a, cpw, split, d->scf16, stepm, fast, lds, grid, st); break;
-    default: launch_kind<SGLQ_KIND_E2M1>(a, cpw, split, 1, 0, fast, lds, grid, st); break;
+    case SGLQ_KIND_U4:
+      launch_kind<SGLQ_KIND_U4>(a, pl.cpw, split, d->scf16, stepm, fast, pl.lds, grid, nthr, st);
+      break;
+    case SGLQ_KIND_U8:
+      launch_kind<SGLQ_KIND_U8>(a, pl.cpw, split, d->scf16, stepm, fast, pl.lds, grid, nthr, st);
+      break;
+    default:
+      launch_kind<SGLQ_KIND_E2M1>(a, pl.cpw, split, 1, 0, fast, pl.lds, grid, nthr, st);
+      break;
   }
   SGLQ_HIP(hipGetLastError());
   return 0;
@@ -516,13 +588,9 @@ extern "C" int sglq_forward(sglq_dev *d, const void *A, int dt, int64_t M, const
                    (long long)d->K);
     return -1;
   }
-  for (int64_t m0 = 0; m0 < M; m0 += 16) {
-    const int64_t mb = M - m0 < 16 ? M - m0 : 16;
-    if (sglq_gemv(d, (const char *)A + m0 * d->K * esz, dt, d->K, mb, bias, C + m0 * d->N, d->N,
-                  st) != 0)
-      return -1;
-  }
-  return 0;
+  if (M > 16) return sglq_gemm(d, A, dt, d->K, M, bias, C, d->N, st);
+  (void)esz;
+  return sglq_gemv(d, A, dt, d->K, M, bias, C, d->N, st);
 fail:
   return -1;
 }

@@ -15,7 +15,8 @@
 //     when every group is a whole number of chunks (META_GROUP, cpg chunks per group), else a
 //     step (META_STEP).  Entry = f16 scale | f16 -(1024 + zero) << 16 when every scale is
 //     f16-exact (4 bytes), else f32 scale | f16 -(1024 + zero) << 32 (8 bytes).
-//   * E2M1 meta: the e8m0 byte of every (column, step), stored [t][16][nsteps] (u8).
+//   * E2M1 meta: the e8m0 byte of every (column, step), stored [t][16][nsteps] (u8), plus the
+//     largest of them per column (colexp), the reference exponent of the prefill GEMM.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -49,10 +50,10 @@ struct sglq_dev {
   void *meta;
   int32_t *kmap;  // [nsteps * 32]
   int32_t *kinv;  // [K]
+  uint8_t *colexp;  // E2M1: largest e8m0 byte (255 excluded) of every column, [ntile * 16]
   // decode GEMV split-K state, sized at build: partial sums [gv_split][16][N] and one arrival
-  // counter per group of 4 tiles (every counter is back at 0 when a launch ends)
-  int gv_cpw;      // chunks per wave (4 or 8)
-  int gv_split;    // K ranges per column group
+  // counter per tile (every counter is back at 0 when a launch ends)
+  int gv_split;    // most K ranges a launch splits over
   float *gv_part;
   int *gv_cnt;
   // prefill GEMM workspace (grown on demand)
@@ -79,6 +80,9 @@ int sglq_ws_reserve(sglq_dev *d, size_t bytes);
 
 // Decode-GEMV launch (gemv.hip): C rows [0, M) with M <= 16.
 int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
+              float *C, int64_t ldc, hipStream_t st);
+// Prefill GEMM launch (gemm.hip): any M; grows the handle's workspace on first use at a size.
+int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
               float *C, int64_t ldc, hipStream_t st);
 // Picks the decode GEMV split for a freshly built weight and allocates its state.
 int sglq_gemv_setup(sglq_dev *d);
