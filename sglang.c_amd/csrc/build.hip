@@ -484,6 +484,7 @@ extern "C" void sglq_free(sglq_dev *d) {
   (void)hipFree(d->kmap);
   (void)hipFree(d->kinv);
   (void)hipFree(d->ws);
+  free(d->moe_tbl);
   free(d);
 }
 

@@ -14,6 +14,8 @@
 //             block scales are folded into the fp4 -> f16 conversion relative to a per-column
 //             exponent (exact for every block within 2^23 of the column's largest), which is
 //             applied at the end.
+#include <string.h>
+
 #include "sglq_dev.hpp"
 
 namespace {
@@ -29,18 +31,26 @@ __device__ __forceinline__ float act_at(const void *A, int dt, int64_t i) {
 
 __device__ __forceinline__ constexpr int kofs4(int i) { return (i >> 1) + 4 * (i & 1); }
 
-// One workgroup (256 threads) per row of Aop (Mpad rows).
+// One workgroup (256 threads) per row of Aop (Mpad rows).  Source row of Aop row m:
+//   MODE 0  A[m]                           (dense)
+//   MODE 1  A[rowmap[m]], zero if < 0       (MoE: token of each expert-sorted row)
+//   MODE 2  a_k = silu(A[m][k]) * A[m][kcols + k], A f32 (MoE: SwiGLU of the gate/up product,
+//           silu(g) = g / (1 + expf(-g)) as reference src/deepseek.c:662-663)
+template <int MODE>
 __global__ __launch_bounds__(256) void k_prep_a(const void *__restrict__ A, int dt, int64_t lda,
                                                 int M, int Mpad, int K, int nsteps,
-                                                const int32_t *__restrict__ kmap, int perm4,
-                                                int split, half8_t *__restrict__ aop,
+                                                const int32_t *__restrict__ kmap,
+                                                const int32_t *__restrict__ rowmap, int kcols,
+                                                int perm4, int split, half8_t *__restrict__ aop,
                                                 int *__restrict__ rowexp) {
   const int m = blockIdx.x;
   const int tid = threadIdx.x;
   __shared__ float red[4];
   const int kp_n = nsteps * 32;
   const int64_t plane = (int64_t)nsteps * 4 * Mpad;  // 16-B items per piece
-  if (m >= M) {
+  int64_t src = m;
+  if constexpr (MODE == 1) src = m < M ? rowmap[m] : -1;
+  if (m >= M || src < 0) {
     const half8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int it = tid; it < nsteps * 4; it += 256) {
       aop[(int64_t)it * Mpad + m] = z;
@@ -49,11 +59,19 @@ __global__ __launch_bounds__(256) void k_prep_a(const void *__restrict__ A, int 
     if (tid == 0) rowexp[m] = 0;
     return;
   }
-  const int64_t rb = (int64_t)m * lda;
+  const int64_t rb = src * lda;
+  auto value = [&](int k) -> float {
+    if constexpr (MODE == 2) {
+      const float g = ((const float *)A)[rb + k];
+      return (g / (1.0f + expf(-g))) * ((const float *)A)[rb + kcols + k];
+    } else {
+      return act_at(A, dt, rb + k);
+    }
+  };
   float mx = 0.f;
   for (int kp = tid; kp < kp_n; kp += 256) {
     const int k = kmap ? kmap[kp] : (kp < K ? kp : -1);
-    if (k >= 0) mx = fmaxf(mx, fabsf(act_at(A, dt, rb + k)));
+    if (k >= 0) mx = fmaxf(mx, fabsf(value(k)));
   }
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
   if ((tid & 63) == 0) red[tid >> 6] = mx;
@@ -67,7 +85,7 @@ __global__ __launch_bounds__(256) void k_prep_a(const void *__restrict__ A, int 
     for (int i = 0; i < 8; i++) {
       const int kp = it * 8 + (perm4 ? kofs4(i) : i);
       const int k = kmap ? kmap[kp] : (kp < K ? kp : -1);
-      const float x = k >= 0 ? ldexpf(act_at(A, dt, rb + k), -e) : 0.f;
+      const float x = k >= 0 ? ldexpf(value(k), -e) : 0.f;
       const _Float16 h = (_Float16)x;
       hi[i] = h;
       lo[i] = (_Float16)(x - (float)h);
@@ -78,9 +96,15 @@ __global__ __launch_bounds__(256) void k_prep_a(const void *__restrict__ A, int 
 }
 
 struct GemmArgs {
+  // dense: one weight; grouped (MoE): weight pointers per expert, picked per row block
   const u32x4_t *codes;
   const void *meta;
   const uint8_t *colexp;  // E2M1: per-column reference exponent (largest e8m0 of the column)
+  const u32x4_t *const *codes_e;
+  const void *const *meta_e;
+  const uint8_t *const *colexp_e;
+  const int4 *segs;       // grouped: per row block {expert, first row, rows, -}
+  const int *nseg;        // grouped: number of row blocks (device scalar)
   const half8_t *aop;    // [np][nsteps][4][Mpad]
   const int *rowexp;
   const float *bias;
@@ -174,7 +198,19 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   const int wm = w & 1, wn = w >> 1;
   const int n16 = lane & 15, kq = lane >> 4;
   const int bn = blockIdx.x % a.nbn, bm = blockIdx.x / a.nbn;
-  const int m0 = bm * BM;
+  int m0 = bm * BM, mend = a.M;
+  const u32x4_t *codes = a.codes;
+  const void *meta = a.meta;
+  const uint8_t *colexp = a.colexp;
+  if (a.segs) {  // grouped: row block bm of the expert-sorted rows
+    if (bm >= *a.nseg) return;
+    const int4 sg = a.segs[bm];
+    m0 = sg.y;
+    mend = sg.y + sg.z;
+    codes = a.codes_e[sg.x];
+    meta = a.meta_e[sg.x];
+    if constexpr (KIND == SGLQ_KIND_E2M1) colexp = a.colexp_e[sg.x];
+  }
   const int64_t plane = (int64_t)a.nsteps * 4 * a.Mpad;
 
   // A tile items of chunk c: item i -> (p, j, kq', row)
@@ -204,21 +240,21 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       const int t = min(t0 + j, a.ntile - 1);
-      bw[j] = __builtin_nontemporal_load(a.codes + ((int64_t)t * a.nchunk + c) * 64 + lane);
+      bw[j] = __builtin_nontemporal_load(codes + ((int64_t)t * a.nchunk + c) * 64 + lane);
       const int64_t mrow = ((int64_t)t * 16 + n16) * a.nmeta;
       if constexpr (E2M1) {
-        bm_[j][0] = ((const uint32_t *)((const uint8_t *)a.meta + mrow))[c];
+        bm_[j][0] = ((const uint32_t *)((const uint8_t *)meta + mrow))[c];
       } else if constexpr (STEPM) {
 #pragma unroll
-        for (int s = 0; s < SPC; s++) bm_[j][s] = ((const MT *)a.meta)[mrow + c * SPC + s];
+        for (int s = 0; s < SPC; s++) bm_[j][s] = ((const MT *)meta)[mrow + c * SPC + s];
       } else {
-        bm_[j][0] = ((const MT *)a.meta)[mrow + g];
+        bm_[j][0] = ((const MT *)meta)[mrow + g];
       }
     }
   };
   if constexpr (E2M1) {
 #pragma unroll
-    for (int j = 0; j < TN; j++) cref[j] = a.colexp[min(t0 + j, a.ntile - 1) * 16 + n16];
+    for (int j = 0; j < TN; j++) cref[j] = colexp[min(t0 + j, a.ntile - 1) * 16 + n16];
   }
 
   float4_t acc[MB][TN], tmp[MB][TN];
@@ -318,7 +354,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int m = m0 + wm * 64 + i * 16 + 4 * kq + r;
-        if (m < a.M) a.C[(int64_t)m * a.ldc + n] = ldexpf(r4[r], a.rowexp[m] + ce) + bv;
+        if (m < mend) a.C[(int64_t)m * a.ldc + n] = ldexpf(r4[r], a.rowexp[m] + ce) + bv;
       }
     }
   }
@@ -374,62 +410,94 @@ void launch_split(const GemmArgs &a, bool split, int scf16, int stepm, int bn, u
 
 }  // namespace
 
-int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
-              float *C, int64_t ldc, hipStream_t st) {
-  const bool split = dt == SGLQ_DT_F32;
-  const int np = split ? 2 : 1;
-  const int64_t Mpad = (M + BM - 1) / BM * BM;
-  const size_t aop_bytes = (size_t)np * d->nsteps * 4 * Mpad * 16;
-  const size_t need = aop_bytes + (size_t)Mpad * sizeof(int) + 256;
-  if (sglq_ws_reserve(d, need) != 0) return -1;
-  half8_t *aop = (half8_t *)d->ws;
-  int *rowexp = (int *)((char *)d->ws + aop_bytes);
-  k_prep_a<<<(unsigned)Mpad, 256, 0, st>>>(A, dt, lda, (int)M, (int)Mpad, (int)d->K,
-                                           (int)d->nsteps, d->kident ? nullptr : d->kmap,
-                                           d->kind == SGLQ_KIND_U4, split, aop, rowexp);
+int sglq_prep_a(const sglq_dev *d, int mode, const void *A, int dt, int64_t lda, int64_t M,
+                int64_t Mpad, const int32_t *rowmap, int kcols, int split, void *aop,
+                int *rowexp, hipStream_t st) {
+  const int32_t *kmap = d->kident ? nullptr : d->kmap;
+  const int perm4 = d->kind == SGLQ_KIND_U4;
+#define SGLQ_PREP(MODE)                                                                     \
+  k_prep_a<MODE><<<(unsigned)Mpad, 256, 0, st>>>(A, dt, lda, (int)M, (int)Mpad, (int)d->K,   \
+                                                  (int)d->nsteps, kmap, rowmap, kcols, perm4, \
+                                                  split, (half8_t *)aop, rowexp)
+  if (mode == 0)
+    SGLQ_PREP(0);
+  else if (mode == 1)
+    SGLQ_PREP(1);
+  else
+    SGLQ_PREP(2);
+#undef SGLQ_PREP
   SGLQ_HIP(hipGetLastError());
-  {
-    // 128-column tiles unless that leaves the chip under-filled
-    const int64_t nbm = Mpad / BM;
-    int bn = 128;
-    if (nbm * ((d->N + 127) / 128) < 512 || d->meta_mode == SGLQ_META_STEP) bn = 64;
-    const int nbn = (int)((d->N + bn - 1) / bn);
-    const int spc = (int)d->spc;
-    const size_t lds = (size_t)2 * np * spc * 4 * BM * 16;
-    GemmArgs a;
-    a.codes = d->codes;
-    a.meta = d->meta;
-    a.colexp = d->colexp;
-    a.aop = aop;
-    a.rowexp = rowexp;
-    a.bias = bias;
-    a.C = C;
-    a.ldc = ldc;
-    a.M = (int)M;
-    a.Mpad = (int)Mpad;
-    a.N = (int)d->N;
-    a.ntile = (int)d->ntile;
-    a.nchunk = (int)d->nchunk;
-    a.nsteps = (int)d->nsteps;
-    a.nmeta = (int)d->nmeta;
-    a.cpg = d->cpg > 0 ? (int)d->cpg : 1;
-    a.nbn = nbn;
-    const unsigned grid = (unsigned)(nbm * nbn);
-    const int stepm = d->meta_mode == SGLQ_META_STEP;
-    switch (d->kind) {
-      case SGLQ_KIND_U4:
-        launch_split<SGLQ_KIND_U4>(a, split, d->scf16, stepm, bn, grid, lds, st);
-        break;
-      case SGLQ_KIND_U8:
-        launch_split<SGLQ_KIND_U8>(a, split, d->scf16, stepm, bn, grid, lds, st);
-        break;
-      default:
-        launch_split<SGLQ_KIND_E2M1>(a, split, 1, 0, bn, grid, lds, st);
-        break;
-    }
-    SGLQ_HIP(hipGetLastError());
-  }
   return 0;
 fail:
   return -1;
+}
+
+size_t sglq_aop_bytes(const sglq_dev *d, int64_t Mpad, int split) {
+  return (size_t)(split ? 2 : 1) * d->nsteps * 4 * Mpad * 16;
+}
+
+int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
+                  const int *rowexp, int64_t M, int64_t Mpad, int64_t nblk, int split,
+                  const float *bias, float *C, int64_t ldc, hipStream_t st) {
+  // 128-column tiles unless that leaves the chip under-filled
+  int bn = 128;
+  if (nblk * ((d->N + 127) / 128) < 512 || d->meta_mode == SGLQ_META_STEP) bn = 64;
+  const int nbn = (int)((d->N + bn - 1) / bn);
+  const size_t lds = (size_t)2 * (split ? 2 : 1) * d->spc * 4 * BM * 16;
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.codes = d->codes;
+  a.meta = d->meta;
+  a.colexp = d->colexp;
+  if (grp) {
+    a.codes_e = (const u32x4_t *const *)grp->codes;
+    a.meta_e = grp->meta;
+    a.colexp_e = grp->colexp;
+    a.segs = (const int4 *)grp->segs;
+    a.nseg = grp->nseg;
+  }
+  a.aop = (const half8_t *)aop;
+  a.rowexp = rowexp;
+  a.bias = bias;
+  a.C = C;
+  a.ldc = ldc;
+  a.M = (int)M;
+  a.Mpad = (int)Mpad;
+  a.N = (int)d->N;
+  a.ntile = (int)d->ntile;
+  a.nchunk = (int)d->nchunk;
+  a.nsteps = (int)d->nsteps;
+  a.nmeta = (int)d->nmeta;
+  a.cpg = d->cpg > 0 ? (int)d->cpg : 1;
+  a.nbn = nbn;
+  const unsigned grid = (unsigned)(nblk * nbn);
+  const int stepm = d->meta_mode == SGLQ_META_STEP;
+  switch (d->kind) {
+    case SGLQ_KIND_U4:
+      launch_split<SGLQ_KIND_U4>(a, split, d->scf16, stepm, bn, grid, lds, st);
+      break;
+    case SGLQ_KIND_U8:
+      launch_split<SGLQ_KIND_U8>(a, split, d->scf16, stepm, bn, grid, lds, st);
+      break;
+    default:
+      launch_split<SGLQ_KIND_E2M1>(a, split, 1, 0, bn, grid, lds, st);
+      break;
+  }
+  SGLQ_HIP(hipGetLastError());
+  return 0;
+fail:
+  return -1;
+}
+
+int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
+              float *C, int64_t ldc, hipStream_t st) {
+  const int split = dt == SGLQ_DT_F32;
+  const int64_t Mpad = (M + BM - 1) / BM * BM;
+  const size_t aop_bytes = sglq_aop_bytes(d, Mpad, split);
+  if (sglq_ws_reserve(d, aop_bytes + (size_t)Mpad * sizeof(int) + 256) != 0) return -1;
+  void *aop = d->ws;
+  int *rowexp = (int *)((char *)d->ws + aop_bytes);
+  if (sglq_prep_a(d, 0, A, dt, lda, M, Mpad, nullptr, 0, split, aop, rowexp, st) != 0)
+    return -1;
+  return sglq_gemm_run(d, nullptr, aop, rowexp, M, Mpad, Mpad / BM, split, bias, C, ldc, st);
 }

@@ -1,11 +1,217 @@
-// moe.hip — routed-expert FFN over device-resident quantized experts.
+// moe.hip — routed-expert FFN over device-resident quantized experts (the expert loop and
+// weighted combine of reference src/deepseek.c:655-677, gate/up fused as in its stacked
+// branch :660-664; routing itself is an input).
+//
+// Launches, all on the caller's stream, no host synchronisation:
+//   k_moe_route   one workgroup: counts (token, slot) pairs per expert, orders them by expert
+//                 (inside an expert by pair index, so the order is deterministic), and writes
+//                 the row-block table of the grouped GEMMs (blocks of <= 128 rows of one expert)
+//   prep (gather) A operands of the expert-sorted rows of h
+//   grouped GEMM  gu = h_rows * Wgu[e]^T for every row block, each with its expert's weights
+//   prep (SwiGLU) A operands of silu(gu[:, :mi]) * gu[:, mi:]
+//   grouped GEMM  o = a * Wdn[e]^T
+//   k_moe_combine out[t] = sum_j w[t,j] * o[row of (t,j)], slots added in order j = 0..k-1
+#include <string.h>
+
 #include "sglq_dev.hpp"
+
+namespace {
+
+constexpr int kMaxExperts = 256;
+
+__global__ __launch_bounds__(1024) void k_moe_route(const int32_t *__restrict__ ids, int P,
+                                                    int k, int n_exp, int32_t *__restrict__ rowmap,
+                                                    int32_t *__restrict__ pos,
+                                                    int *__restrict__ segs,
+                                                    int *__restrict__ nseg) {
+  __shared__ int run[kMaxExperts];       // next free row of each expert
+  __shared__ int wc[16][kMaxExperts];    // per-wave counts of the current block of pairs
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  for (int e = tid; e < n_exp; e += 1024) run[e] = 0;
+  for (int r = tid; r < P; r += 1024) rowmap[r] = -1;  // rows past the routed pairs: zero rows
+  __syncthreads();
+  for (int p = tid; p < P; p += 1024) {
+    const int e = ids[p];
+    if (e >= 0 && e < n_exp) atomicAdd(&run[e], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {  // exclusive scan + row-block table
+    int off = 0, nb = 0;
+    for (int e = 0; e < n_exp; e++) {
+      const int c = run[e];
+      for (int r = 0; r < c; r += SGLQ_GEMM_BM) {
+        segs[nb * 4 + 0] = e;
+        segs[nb * 4 + 1] = off + r;
+        segs[nb * 4 + 2] = min(SGLQ_GEMM_BM, c - r);
+        segs[nb * 4 + 3] = 0;
+        nb++;
+      }
+      run[e] = off;
+      off += c;
+    }
+    *nseg = nb;
+  }
+  __syncthreads();
+  const uint64_t lt = (1ull << lane) - 1ull;
+  for (int b = 0; b < P; b += 1024) {
+    const int p = b + tid;
+    const int e = p < P ? ids[p] : -1;
+    const bool ok = e >= 0 && e < n_exp;
+    int rank = 0;
+    for (int ee = 0; ee < n_exp; ee++) {
+      const uint64_t m = __ballot(ok && e == ee);
+      if (ok && e == ee) rank = __popcll(m & lt);
+      if (lane == 0) wc[w][ee] = __popcll(m);
+    }
+    __syncthreads();
+    if (p < P) {
+      if (ok) {
+        int dst = run[e] + rank;
+        for (int ww = 0; ww < w; ww++) dst += wc[ww][e];
+        rowmap[dst] = p / k;
+        pos[p] = dst;
+      } else {
+        pos[p] = -1;
+      }
+    }
+    __syncthreads();
+    for (int ee = tid; ee < n_exp; ee += 1024) {
+      int s = 0;
+      for (int ww = 0; ww < 16; ww++) s += wc[ww][ee];
+      run[ee] += s;
+    }
+    __syncthreads();
+  }
+}
+
+// out[t][c] = ((0 + w0 o0) + w1 o1) + ... in slot order, products and sums rounded separately
+// as the reference's orow[i] += w * o[i] (reference src/deepseek.c:675-676)
+__global__ void k_moe_combine(const float *__restrict__ o, int64_t ldo,
+                              const int32_t *__restrict__ pos, const float *__restrict__ wts,
+                              int k, int E, float *__restrict__ out) {
+  const int t = blockIdx.y;
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= E) return;
+  float acc = 0.f;
+  for (int j = 0; j < k; j++) {
+    const int r = pos[t * k + j];
+    if (r < 0) continue;
+    acc = __fadd_rn(acc, __fmul_rn(wts[t * k + j], o[(int64_t)r * ldo + c]));
+  }
+  out[(int64_t)t * E + c] = acc;
+}
+
+bool same_format(const sglq_dev *a, const sglq_dev *b) {
+  return a->N == b->N && a->K == b->K && a->kind == b->kind && a->scf16 == b->scf16 &&
+         a->meta_mode == b->meta_mode && a->nchunk == b->nchunk && a->nmeta == b->nmeta &&
+         a->cpg == b->cpg && a->kident == b->kident && a->dev == b->dev;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace
 
 extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down, int n_exp,
                                 const void *h, int h_dtype, int64_t T, const int32_t *topk_ids,
                                 const float *topk_w, int k, float *out, void *stream) {
-  (void)gate_up; (void)down; (void)n_exp; (void)h; (void)h_dtype; (void)T; (void)topk_ids;
-  (void)topk_w; (void)k; (void)out; (void)stream;
-  sglq_log_error("qmoe: not available in this build");
+  hipStream_t st = (hipStream_t)stream;
+  sglq_dev *g0 = gate_up[0], *d0 = down[0];
+  if (n_exp > kMaxExperts) {
+    sglq_log_error("qmoe: %d experts (at most %d)", n_exp, kMaxExperts);
+    return -1;
+  }
+  if (g0->N % 2 != 0 || d0->N != g0->K || d0->K != g0->N / 2) {
+    sglq_log_error("qmoe: gate_up [%lld,%lld] / down [%lld,%lld] do not form an expert FFN",
+                   (long long)g0->N, (long long)g0->K, (long long)d0->N, (long long)d0->K);
+    return -1;
+  }
+  for (int e = 0; e < n_exp; e++) {
+    if (!same_format(gate_up[e], g0) || !same_format(down[e], d0)) {
+      sglq_log_error("qmoe: expert %d differs in shape or format from expert 0", e);
+      return -1;
+    }
+  }
+  if (!g0->kident || !d0->kident) {
+    sglq_log_error("qmoe: act-order (g_idx) experts are not supported");
+    return -1;
+  }
+  if (T == 0) return 0;
+  {
+    const int64_t E = g0->K, mi = d0->K, P = T * k;
+    const int64_t maxblk = (P + SGLQ_GEMM_BM - 1) / SGLQ_GEMM_BM + n_exp;
+    const int64_t Mpad = (P + SGLQ_GEMM_BM - 1) / SGLQ_GEMM_BM * SGLQ_GEMM_BM + SGLQ_GEMM_BM;
+    const int split1 = h_dtype == SGLQ_DT_F32;
+    // workspace (kept in expert 0's gate_up handle)
+    size_t off = 0;
+    const size_t o_ptr = off; off = align256(off + (size_t)6 * n_exp * sizeof(void *));
+    const size_t o_rowmap = off; off = align256(off + (size_t)Mpad * 4);
+    const size_t o_pos = off; off = align256(off + (size_t)P * 4);
+    const size_t o_segs = off; off = align256(off + (size_t)maxblk * 16);
+    const size_t o_nseg = off; off = align256(off + 4);
+    const size_t o_aop1 = off; off = align256(off + sglq_aop_bytes(g0, Mpad, split1));
+    const size_t o_rexp1 = off; off = align256(off + (size_t)Mpad * 4);
+    const size_t o_gu = off; off = align256(off + (size_t)Mpad * 2 * mi * 4);
+    const size_t o_aop2 = off; off = align256(off + sglq_aop_bytes(d0, Mpad, 1));
+    const size_t o_rexp2 = off; off = align256(off + (size_t)Mpad * 4);
+    const size_t o_o = off; off = align256(off + (size_t)Mpad * E * 4);
+    if (sglq_ws_reserve(g0, off) != 0) return -1;
+    char *ws = (char *)g0->ws;
+    // expert pointer tables: uploaded when they differ from the last upload
+    const void **hp = (const void **)malloc((size_t)6 * n_exp * sizeof(void *));
+    if (!hp) return -1;
+    for (int e = 0; e < n_exp; e++) {
+      hp[0 * n_exp + e] = gate_up[e]->codes;
+      hp[1 * n_exp + e] = gate_up[e]->meta;
+      hp[2 * n_exp + e] = gate_up[e]->colexp;
+      hp[3 * n_exp + e] = down[e]->codes;
+      hp[4 * n_exp + e] = down[e]->meta;
+      hp[5 * n_exp + e] = down[e]->colexp;
+    }
+    const size_t tbl = (size_t)6 * n_exp * sizeof(void *);
+    if (g0->moe_tbl_bytes != tbl || !g0->moe_tbl || memcmp(g0->moe_tbl, hp, tbl) != 0 ||
+        g0->moe_tbl_ws != g0->ws) {
+      if (hipMemcpy(ws + o_ptr, hp, tbl, hipMemcpyHostToDevice) != hipSuccess) {
+        sglq_log_error("qmoe: uploading the expert table failed");
+        free(hp);
+        return -1;
+      }
+      free(g0->moe_tbl);
+      g0->moe_tbl = hp;
+      g0->moe_tbl_bytes = tbl;
+      g0->moe_tbl_ws = g0->ws;
+    } else {
+      free(hp);
+    }
+    const void *const *dp = (const void *const *)(ws + o_ptr);
+    int32_t *rowmap = (int32_t *)(ws + o_rowmap);
+    int32_t *pos = (int32_t *)(ws + o_pos);
+    int *segs = (int *)(ws + o_segs);
+    int *nseg = (int *)(ws + o_nseg);
+    float *gu = (float *)(ws + o_gu);
+    float *o = (float *)(ws + o_o);
+    k_moe_route<<<1, 1024, 0, st>>>(topk_ids, (int)P, k, n_exp, rowmap, pos, segs, nseg);
+    SGLQ_HIP(hipGetLastError());
+    // rows of Mpad beyond P: rowmap entries are never read (prep zeroes rows >= M)
+    if (sglq_prep_a(g0, 1, h, h_dtype, E, P, Mpad, rowmap, 0, split1, ws + o_aop1,
+                    (int *)(ws + o_rexp1), st) != 0)
+      return -1;
+    sglq_group g1 = {dp, dp + n_exp, (const uint8_t *const *)(dp + 2 * n_exp), segs, nseg};
+    if (sglq_gemm_run(g0, &g1, ws + o_aop1, (const int *)(ws + o_rexp1), P, Mpad, maxblk,
+                      split1, nullptr, gu, 2 * mi, st) != 0)
+      return -1;
+    if (sglq_prep_a(d0, 2, gu, SGLQ_DT_F32, 2 * mi, P, Mpad, nullptr, (int)mi, 1, ws + o_aop2,
+                    (int *)(ws + o_rexp2), st) != 0)
+      return -1;
+    sglq_group g2 = {dp + 3 * n_exp, dp + 4 * n_exp, (const uint8_t *const *)(dp + 5 * n_exp),
+                     segs, nseg};
+    if (sglq_gemm_run(d0, &g2, ws + o_aop2, (const int *)(ws + o_rexp2), P, Mpad, maxblk, 1,
+                      nullptr, o, E, st) != 0)
+      return -1;
+    dim3 grid((unsigned)((E + 255) / 256), (unsigned)T);
+    k_moe_combine<<<grid, 256, 0, st>>>(o, E, pos, topk_w, k, (int)E, out);
+    SGLQ_HIP(hipGetLastError());
+  }
+  return 0;
+fail:
   return -1;
 }

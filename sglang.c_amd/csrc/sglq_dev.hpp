@@ -56,9 +56,13 @@ struct sglq_dev {
   int gv_split;    // most K ranges a launch splits over
   float *gv_part;
   int *gv_cnt;
-  // prefill GEMM workspace (grown on demand)
+  // prefill GEMM / MoE workspace (grown on demand)
   void *ws;
   size_t ws_bytes;
+  // MoE: host copy of the expert pointer table last uploaded into ws (re-uploaded on change)
+  void *moe_tbl;
+  size_t moe_tbl_bytes;
+  void *moe_tbl_ws;
 };
 
 #define SGLQ_HIP(expr)                                                                    \
@@ -84,6 +88,26 @@ int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
 // Prefill GEMM launch (gemm.hip): any M; grows the handle's workspace on first use at a size.
 int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
               float *C, int64_t ldc, hipStream_t st);
+
+// Grouped-GEMM building blocks (gemm.hip), used by the MoE path.
+constexpr int SGLQ_GEMM_BM = 128;  // rows per GEMM row block
+struct sglq_group {               // per-expert weights (device arrays) + device row-block table
+  const void *const *codes;       // [n_exp] u32x4_t*
+  const void *const *meta;        // [n_exp]
+  const uint8_t *const *colexp;   // [n_exp] (MXFP4)
+  const int *segs;                // [max blocks][4] {expert, first row, rows, 0}
+  const int *nseg;                // blocks in use (device scalar)
+};
+// A operands of Mpad rows into aop (sglq_aop_bytes) + row exponents; mode 0 dense rows,
+// 1 rows gathered through rowmap (-1 = zero row), 2 silu(A[m][k]) * A[m][kcols + k] (f32 A).
+int sglq_prep_a(const sglq_dev *d, int mode, const void *A, int dt, int64_t lda, int64_t M,
+                int64_t Mpad, const int32_t *rowmap, int kcols, int split, void *aop,
+                int *rowexp, hipStream_t st);
+size_t sglq_aop_bytes(const sglq_dev *d, int64_t Mpad, int split);
+// nblk row blocks (dense: block b = rows [128b, 128b+128); grouped: from grp->segs).
+int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop, const int *rowexp,
+                  int64_t M, int64_t Mpad, int64_t nblk, int split, const float *bias, float *C,
+                  int64_t ldc, hipStream_t st);
 // Picks the decode GEMV split for a freshly built weight and allocates its state.
 int sglq_gemv_setup(sglq_dev *d);
 

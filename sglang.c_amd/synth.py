@@ -47,8 +47,26 @@ def quantize_groups(W, G, bits=4, g_idx=None, sym=False):
     Per group: s = (max - min) / (2^bits - 1) rounded to fp16, z = clamp(round(-min/s)),
     q = clamp(round(w/s) + z).  With sym=True z = 2^(bits-1) and s = absmax / (2^(bits-1)-1)."""
     N, K = W.shape
+    Ge = G if G > 0 else K
+    if g_idx is None and K % Ge == 0:  # contiguous groups: the same arithmetic, vectorised
+        w = W.reshape(N, K // Ge, Ge).astype(np.float32)
+        qmax = (1 << bits) - 1
+        if sym:
+            s = (np.abs(w).max(axis=2) / ((1 << (bits - 1)) - 1)).astype(np.float16)
+            s = s.astype(np.float32)
+            s[s == 0] = 1.0
+            z = np.full(s.shape, 1 << (bits - 1), np.float32)
+        else:
+            lo = np.minimum(w.min(axis=2), 0)
+            hi = np.maximum(w.max(axis=2), 0)
+            s = ((hi - lo) / qmax).astype(np.float16).astype(np.float32)
+            s[s == 0] = 1.0
+            z = np.clip(np.round(-lo / s), 0, qmax)
+        q = np.clip(np.round(w / s[:, :, None]) + z[:, :, None], 0, qmax)
+        return (q.reshape(N, K).astype(np.uint8), np.ascontiguousarray(z.T).astype(np.uint8),
+                np.ascontiguousarray(s.T))
     if g_idx is None:
-        g_idx = np.arange(K) // (G if G > 0 else K)
+        g_idx = np.arange(K) // Ge
     ng = int(g_idx.max()) + 1
     qmax = (1 << bits) - 1
     codes = np.zeros((N, K), np.uint8)
@@ -222,3 +240,22 @@ def quant_rows_i8(W):
     q[amax <= 0] = 0
     scale[amax <= 0] = 0
     return q, scale
+
+
+# ---------------------------------------------------------------------------------------
+# routed MoE inputs: top-k experts uniform without replacement per token,
+# weights = softmax of N(0,1) logits over the k picks
+# ---------------------------------------------------------------------------------------
+def moe_routing(seed, T, n_exp, k):
+    g = rng(seed)
+    ids = np.stack([g.permutation(n_exp)[:k] for _ in range(T)]).astype(np.int32)
+    logits = g.standard_normal((T, k))
+    w = np.exp(logits - logits.max(axis=1, keepdims=True))
+    return ids, (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+def gptq_expert(seed, N, K, G=128):
+    """One GPTQ int4 g128 weight [N, K] ~ N(0, 0.02): (qweight, qzeros, scales)."""
+    c, z, s = quantize_groups(normal(seed, (N, K), 0.02), G)
+    qw, qz = gptq_pack(c, z)
+    return qw, qz, s

@@ -1,0 +1,70 @@
+"""Routed-expert FFN on the GPU (sgl_qmoe_forward) against the reference CPU composition
+(oracle: dequant every expert, then reference src/deepseek.c:655-677 per token and slot).
+Tolerance: max|y - y_ref| / max|y_ref| <= 1e-3."""
+import numpy as np
+import pytest
+
+import synth
+from linear_cases import rel_err
+from oracle.oracle import make_cfg as ocfg
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _experts(orc, n_exp, E, mi, seed):
+    import sgl_qlinear as q
+    cfg = dict(method=2, bits=4, group_size=128, zero_point=1)
+    gu, dn, wgu, wdn = [], [], [], []
+    for e in range(n_exp):
+        for (N, K, lst, wl, sd) in ((2 * mi, E, gu, wgu, seed + 2 * e),
+                                    (E, mi, dn, wdn, seed + 2 * e + 1)):
+            qw, qz, s = synth.gptq_expert(sd, N, K)
+            lst.append(q.QLinear.from_awq_gptq(q.make_cfg(**cfg), qw, s, N, K, qzeros=qz))
+            rc, W = orc.dequant(ocfg(**cfg), qw, s, N, K, qzeros=qz)
+            assert rc == 0
+            wl.append(W)
+    return gu, dn, wgu, wdn
+
+
+def _check(orc, n_exp, E, mi, T, k, seed, dtypes=("bf16", "f32"), drop=False):
+    import torch
+    import sgl_qlinear as q
+    gu, dn, wgu, wdn = _experts(orc, n_exp, E, mi, seed)
+    ids, wts = synth.moe_routing(seed + 999, T, n_exp, k)
+    if drop:  # unrouted slots (id -1) are skipped
+        ids[::3, -1] = -1
+    h = synth.normal(seed + 1000, (T, E))
+    for dt in dtypes:
+        if dt == "bf16":
+            hb = synth.bf16_bits_to_f32(synth.to_bf16_bits(h))
+            th = torch.from_numpy(hb).cuda().to(torch.bfloat16)
+        else:
+            hb, th = h, torch.from_numpy(h).cuda()
+        print(f"[gpu] moe n_exp={n_exp} E={E} mi={mi} T={T} k={k} {dt}", flush=True)
+        y = q.qmoe_forward(gu, dn, th, torch.from_numpy(ids).cuda(),
+                           torch.from_numpy(wts).cuda()).cpu().numpy()
+        ref = orc.moe_ffn(hb, wgu, wdn, ids, wts)
+        e = rel_err(y, ref)
+        assert e <= TOL, (dt, e)
+        y2 = q.qmoe_forward(gu, dn, th, torch.from_numpy(ids).cuda(),
+                            torch.from_numpy(wts).cuda()).cpu().numpy()
+        assert np.array_equal(y, y2), "MoE forward is not deterministic"
+
+
+def test_moe_small(orc):
+    _check(orc, 8, 256, 128, 20, 2, seed=31)
+
+
+def test_moe_unrouted_slots(orc):
+    _check(orc, 6, 256, 256, 9, 3, seed=41, dtypes=("f32",), drop=True)
+
+
+def test_moe_decode_deepseek_shape(orc):
+    """BASELINE config 5, decode: one token, 6 of 64 experts, hidden 2048, inter 1408."""
+    _check(orc, 64, 2048, 1408, 1, 6, seed=0x5EED0005, dtypes=("bf16",))
+
+
+def test_moe_prefill_deepseek_shape(orc):
+    """BASELINE config 5, prefill: 512 tokens, top-6 of 64 experts, hidden 2048, inter 1408."""
+    _check(orc, 64, 2048, 1408, 512, 6, seed=0x5EED0005, dtypes=("bf16",))
