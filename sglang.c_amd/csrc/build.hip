@@ -171,6 +171,9 @@ __global__ void k_check_f16(const float *__restrict__ s, int64_t n, int *__restr
   if (i >= n) return;
   const float v = s[i];
   if ((float)(_Float16)v != v) atomicOr(flag, 1);
+  // bit 1: (q - z) * s can leave f16's normal range (|q - z| <= 256)
+  const float a = fabsf(v);
+  if (!(a == 0.f || (a >= 0x1p-14f && a <= 128.f))) atomicOr(flag, 2);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -432,7 +435,8 @@ static sglq_dev *build_impl(const sglq_plan *p, const void *qw, const void *qz, 
       k_check_f16<<<sglq_blocks(GN, T), T>>>(ds, GN, flag);
       int hflag = 1;
       SGLQ_HIP(hipMemcpy(&hflag, flag, 4, hipMemcpyDeviceToHost));
-      d->scf16 = hflag == 0;
+      d->scf16 = (hflag & 1) == 0;
+      d->prescale = hflag == 0;
       const int64_t nm = d->ntile * 16 * d->nmeta;
       SGLQ_HIP(hipMalloc(&d->meta, nm * (d->scf16 ? 4 : 8)));
       k_pack_meta<<<sglq_blocks(nm, T), T>>>(

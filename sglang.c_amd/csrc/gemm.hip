@@ -14,13 +14,13 @@
 //             block scales are folded into the fp4 -> f16 conversion relative to a per-column
 //             exponent (exact for every block within 2^23 of the column's largest), which is
 //             applied at the end.
+#include <stdlib.h>
 #include <string.h>
 
 #include "sglq_dev.hpp"
 
 namespace {
 
-constexpr int BM = 128;
 
 __device__ __forceinline__ float act_at(const void *A, int dt, int64_t i) {
   if (dt == SGLQ_DT_F32) return ((const float *)A)[i];
@@ -183,22 +183,39 @@ __device__ __forceinline__ float e8m0_rel(uint32_t e, int ref) {
   return (e == 255u || d <= 0) ? 0.f : __uint_as_float((uint32_t)d << 23);
 }
 
-template <int KIND, bool SPLIT, bool SCF16, bool STEPM, int BN>
+// Non-temporal 128-bit load through a global (not flat) pointer: weights are streamed once.
+__device__ __forceinline__ u32x4_t ldg_nt(const u32x4_t *p) {
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4_t *)p);
+}
+template <class T>
+__device__ __forceinline__ T ldg(const T *p) {
+  return *(const __attribute__((address_space(1))) T *)p;
+}
+
+// Prefill GEMM.  PS ("prescaled"): the group scale is multiplied into the f16 weight in the
+// unpack ((q - z) exact, then one f16 rounding of (q - z) * s) and the MFMAs accumulate C
+// directly; used when every scale is an f16 value whose products stay normal f16.  Otherwise
+// (f32 scales, per-step groups) the exact form keeps per-chunk partial sums and applies the
+// fp32 scale to them.  MXFP4 always accumulates directly (scales folded exactly).  MB 16-row
+// blocks per wave: the workgroup covers 32*MB rows x BN columns with 2 x 2 waves.
+template <int KIND, bool SPLIT, bool SCF16, bool STEPM, int BN, bool PS, int MB>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
   constexpr int NP = SPLIT ? 2 : 1;
   constexpr int TN = BN / 32;  // 16-column tiles per wave
-  constexpr int MB = 4;        // 16-row blocks per wave (64 rows)
+  constexpr int BMR = 32 * MB; // rows per workgroup
   constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
-  constexpr int ITEMS = NP * SPC * 4 * BM;  // 16-B A items per chunk
+  constexpr bool DIRECT = PS || E2M1;       // accumulate C directly (no per-chunk partials)
+  constexpr int ITEMS = NP * SPC * 4 * BMR; // 16-B A items per chunk
   constexpr int IPT = ITEMS / 256;          // per thread
-  extern __shared__ half8_t s_a[];          // [2][NP][SPC][4][BM]
+  constexpr int RPI = 256 / BMR;            // item rows per 256 threads (1 or 2)
+  extern __shared__ half8_t s_a[];          // [2][NP][SPC][4][BMR]
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int wm = w & 1, wn = w >> 1;
   const int n16 = lane & 15, kq = lane >> 4;
   const int bn = blockIdx.x % a.nbn, bm = blockIdx.x / a.nbn;
-  int m0 = bm * BM, mend = a.M;
+  int m0 = bm * BMR, mend = a.M;
   const u32x4_t *codes = a.codes;
   const void *meta = a.meta;
   const uint8_t *colexp = a.colexp;
@@ -211,18 +228,21 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     meta = a.meta_e[sg.x];
     if constexpr (KIND == SGLQ_KIND_E2M1) colexp = a.colexp_e[sg.x];
   }
-  const int64_t plane = (int64_t)a.nsteps * 4 * a.Mpad;
 
-  // A tile items of chunk c: item i -> (p, j, kq', row)
-  auto a_src = [&](int c, int i) -> const half8_t * {
-    const int row = i % BM, r = i / BM;  // r = (p * SPC + j) * 4 + kq'
+  // A tile of chunk c, item q of this thread: row tid % BMR, slot r = q * RPI + tid / BMR with
+  // r = (p * SPC + j) * 4 + kq'
+  const int64_t plane = (int64_t)a.nsteps * 4 * a.Mpad;
+  const int64_t cstride = (int64_t)SPC * 4 * a.Mpad;  // items per chunk along the K steps
+  const half8_t *abase = a.aop + m0 + (tid % BMR) + (int64_t)(tid / BMR) * a.Mpad;
+  auto a_off = [&](int q) -> int64_t {  // uniform part of item q's offset
+    const int r = q * RPI;
     const int p = r / (SPC * 4), sj = r % (SPC * 4);
-    return a.aop + p * plane + ((int64_t)(c * SPC) * 4 + sj) * a.Mpad + m0 + row;
+    return p * plane + (int64_t)sj * a.Mpad;
   };
   half8_t areg[IPT];
   auto load_a = [&](int c) {
 #pragma unroll
-    for (int q = 0; q < IPT; q++) areg[q] = *a_src(c, tid + 256 * q);
+    for (int q = 0; q < IPT; q++) areg[q] = ldg(abase + a_off(q) + c * cstride);
   };
   auto store_a = [&](int buf) {
 #pragma unroll
@@ -233,22 +253,29 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   const int t0 = bn * (BN / 16) + wn * TN;
   using MT = typename std::conditional<E2M1, uint32_t, meta_t<SCF16>>::type;
   constexpr int NMV = STEPM ? SPC : 1;
+  const u32x4_t *bptr[TN];
+  const MT *mptr[TN];
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const int t = min(t0 + j, a.ntile - 1);
+    bptr[j] = codes + (int64_t)t * a.nchunk * 64 + lane;
+    mptr[j] = (const MT *)((const char *)meta +
+                           ((int64_t)t * 16 + n16) * a.nmeta * (E2M1 ? 1 : (int)sizeof(MT)));
+  }
   u32x4_t bw[TN];
   MT bm_[TN][NMV];
   int cref[TN];
   auto load_b = [&](int c, int g) {
 #pragma unroll
     for (int j = 0; j < TN; j++) {
-      const int t = min(t0 + j, a.ntile - 1);
-      bw[j] = __builtin_nontemporal_load(codes + ((int64_t)t * a.nchunk + c) * 64 + lane);
-      const int64_t mrow = ((int64_t)t * 16 + n16) * a.nmeta;
+      bw[j] = ldg_nt(bptr[j] + c * 64);
       if constexpr (E2M1) {
-        bm_[j][0] = ((const uint32_t *)((const uint8_t *)meta + mrow))[c];
+        bm_[j][0] = ldg((const uint32_t *)mptr[j] + c);
       } else if constexpr (STEPM) {
 #pragma unroll
-        for (int s = 0; s < SPC; s++) bm_[j][s] = ((const MT *)meta)[mrow + c * SPC + s];
+        for (int s = 0; s < SPC; s++) bm_[j][s] = ldg(mptr[j] + c * SPC + s);
       } else {
-        bm_[j][0] = ((const MT *)meta)[mrow + g];
+        bm_[j][0] = ldg(mptr[j] + g);
       }
     }
   };
@@ -257,16 +284,20 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     for (int j = 0; j < TN; j++) cref[j] = colexp[min(t0 + j, a.ntile - 1) * 16 + n16];
   }
 
-  float4_t acc[MB][TN], tmp[MB][TN];
+  float4_t acc[MB][TN];
+  float4_t tmp[DIRECT ? 1 : MB][DIRECT ? 1 : TN];
 #pragma unroll
   for (int i = 0; i < MB; i++)
 #pragma unroll
-    for (int j = 0; j < TN; j++) {
-      acc[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
-      tmp[i][j] = acc[i][j];
-    }
+    for (int j = 0; j < TN; j++) acc[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  if constexpr (!DIRECT) {
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) tmp[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  }
 
-  int g = 0, gr = 0;  // group of the current chunk (META_GROUP), chunks into it
+  int g = 0, gr = 0;  // group of the next chunk (META_GROUP), chunks into it
   load_a(0);
   load_b(0, 0);
   store_a(0);
@@ -289,43 +320,63 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
       load_a(c + 1);
       load_b(c + 1, g);
     }
-    // compute chunk c from LDS buffer buf and registers cw / cm
-    const half8_t *sa = s_a + buf * ITEMS + wm * 64 + n16;
+    const half8_t *sa = s_a + buf * ITEMS + wm * (16 * MB) + n16;
     float sc[TN];
-    half2_t zA[TN], zB[TN];
+    half2_t zA[TN], zB[TN], s2[TN];
     if constexpr (!E2M1 && !STEPM) {
 #pragma unroll
-      for (int j = 0; j < TN; j++) decode_meta<SCF16>(cm[j][0], sc[j], zA[j], zB[j]);
+      for (int j = 0; j < TN; j++) {
+        decode_meta<SCF16>(cm[j][0], sc[j], zA[j], zB[j]);
+        if constexpr (PS) {
+          const _Float16 hs = (_Float16)sc[j];
+          s2[j] = (half2_t){hs, hs};
+        }
+      }
     }
 #pragma unroll
     for (int s = 0; s < SPC; s++) {
-      half8_t av[NP][MB];
-#pragma unroll
-      for (int p = 0; p < NP; p++)
-#pragma unroll
-        for (int i = 0; i < MB; i++) av[p][i] = sa[((p * SPC + s) * 4 + kq) * BM + i * 16];
+      half8_t b[TN];
 #pragma unroll
       for (int j = 0; j < TN; j++) {
         float fsc = 1.f;
         if constexpr (STEPM) decode_meta<SCF16>(cm[j][s], sc[j], zA[j], zB[j]);
         if constexpr (E2M1) fsc = e8m0_rel((cm[j][0] >> (8 * s)) & 255u, cref[j]);
-        const half8_t b = unpack_b<KIND>(cw[j], s, zA[j], zB[j], fsc);
+        b[j] = unpack_b<KIND>(cw[j], s, zA[j], zB[j], fsc);
+        if constexpr (PS && !E2M1) {
+          H8 u;
+          u.v = b[j];
 #pragma unroll
-        for (int i = 0; i < MB; i++) {
-#pragma unroll
-          for (int p = 0; p < NP; p++)
-            tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[p][i], b, tmp[i][j], 0, 0, 0);
+          for (int h = 0; h < 4; h++) u.h[h] = u.h[h] * s2[j];
+          b[j] = u.v;
         }
-        if constexpr (STEPM) {
+      }
 #pragma unroll
-          for (int i = 0; i < MB; i++) {
-            acc[i][j] += sc[j] * tmp[i][j];
-            tmp[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < MB; i++) {
+        half8_t av[NP];
+#pragma unroll
+        for (int p = 0; p < NP; p++) av[p] = sa[((p * SPC + s) * 4 + kq) * BMR + i * 16];
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+#pragma unroll
+          for (int p = 0; p < NP; p++) {
+            if constexpr (DIRECT)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[p], b[j], acc[i][j], 0, 0, 0);
+            else
+              tmp[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[p], b[j], tmp[i][j], 0, 0, 0);
           }
         }
       }
+      if constexpr (STEPM && !DIRECT) {
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+          for (int j = 0; j < TN; j++) {
+            acc[i][j] += sc[j] * tmp[i][j];
+            tmp[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+          }
+      }
     }
-    if constexpr (!STEPM && !E2M1) {
+    if constexpr (!STEPM && !DIRECT) {
 #pragma unroll
       for (int i = 0; i < MB; i++)
 #pragma unroll
@@ -341,7 +392,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   }
 
   // epilogue: lane holds rows 4*kq + r of each 16-row block, column n16 of each tile.  MXFP4
-  // sums stay in tmp (block scales were folded into the weights) and take the column exponent.
+  // sums take the column exponent.
 #pragma unroll
   for (int j = 0; j < TN; j++) {
     const int n = (t0 + j) * 16 + n16;
@@ -350,28 +401,27 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const int ce = E2M1 ? cref[j] - 127 : 0;
 #pragma unroll
     for (int i = 0; i < MB; i++) {
-      const float4_t r4 = E2M1 ? tmp[i][j] : acc[i][j];
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const int m = m0 + wm * 64 + i * 16 + 4 * kq + r;
-        if (m < mend) a.C[(int64_t)m * a.ldc + n] = ldexpf(r4[r], a.rowexp[m] + ce) + bv;
+        const int m = m0 + wm * (16 * MB) + i * 16 + 4 * kq + r;
+        if (m < mend) a.C[(int64_t)m * a.ldc + n] = ldexpf(acc[i][j][r], a.rowexp[m] + ce) + bv;
       }
     }
   }
 }
 
-template <int KIND, bool SPLIT, bool SCF16, bool STEPM>
+template <int KIND, bool SPLIT, bool SCF16, bool STEPM, bool PS, int MB>
 void launch_bn(const GemmArgs &a, int bn, unsigned grid, size_t lds, hipStream_t st) {
   // LDS beyond 64 KiB must be enabled per kernel once (160 KiB on gfx950)
   static bool raised128 = false, raised64 = false;
   if (bn == 128) {
-    auto f = k_gemm<KIND, SPLIT, SCF16, STEPM, 128>;
+    auto f = k_gemm<KIND, SPLIT, SCF16, STEPM, 128, PS, MB>;
     if (!raised128)
       raised128 = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       160 * 1024) == hipSuccess;
     f<<<grid, 256, lds, st>>>(a);
   } else {
-    auto f = k_gemm<KIND, SPLIT, SCF16, STEPM, 64>;
+    auto f = k_gemm<KIND, SPLIT, SCF16, STEPM, 64, PS, MB>;
     if (!raised64)
       raised64 = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      160 * 1024) == hipSuccess;
@@ -379,33 +429,41 @@ void launch_bn(const GemmArgs &a, int bn, unsigned grid, size_t lds, hipStream_t
   }
 }
 
+// variant: 0 exact (per-chunk partials), 1 prescaled MB=4, 2 prescaled MB=8
 template <int KIND, bool SPLIT>
-void launch_meta(const GemmArgs &a, int scf16, int stepm, int bn, unsigned grid, size_t lds,
-                 hipStream_t st) {
+void launch_meta(const GemmArgs &a, int scf16, int stepm, int variant, int bn, unsigned grid,
+                 size_t lds, hipStream_t st) {
   if constexpr (KIND == SGLQ_KIND_E2M1) {
-    launch_bn<KIND, SPLIT, true, false>(a, bn, grid, lds, st);
+    if (variant == 2)
+      launch_bn<KIND, SPLIT, true, false, true, 8>(a, bn, grid, lds, st);
+    else
+      launch_bn<KIND, SPLIT, true, false, true, 4>(a, bn, grid, lds, st);
   } else {
-    if (scf16) {
+    if (variant == 2) {
+      launch_bn<KIND, SPLIT, true, false, true, 8>(a, bn, grid, lds, st);
+    } else if (variant == 1) {
+      launch_bn<KIND, SPLIT, true, false, true, 4>(a, bn, grid, lds, st);
+    } else if (scf16) {
       if (stepm)
-        launch_bn<KIND, SPLIT, true, true>(a, bn, grid, lds, st);
+        launch_bn<KIND, SPLIT, true, true, false, 4>(a, bn, grid, lds, st);
       else
-        launch_bn<KIND, SPLIT, true, false>(a, bn, grid, lds, st);
+        launch_bn<KIND, SPLIT, true, false, false, 4>(a, bn, grid, lds, st);
     } else {
       if (stepm)
-        launch_bn<KIND, SPLIT, false, true>(a, bn, grid, lds, st);
+        launch_bn<KIND, SPLIT, false, true, false, 4>(a, bn, grid, lds, st);
       else
-        launch_bn<KIND, SPLIT, false, false>(a, bn, grid, lds, st);
+        launch_bn<KIND, SPLIT, false, false, false, 4>(a, bn, grid, lds, st);
     }
   }
 }
 
 template <int KIND>
-void launch_split(const GemmArgs &a, bool split, int scf16, int stepm, int bn, unsigned grid,
-                  size_t lds, hipStream_t st) {
+void launch_split(const GemmArgs &a, bool split, int scf16, int stepm, int variant, int bn,
+                  unsigned grid, size_t lds, hipStream_t st) {
   if (split)
-    launch_meta<KIND, true>(a, scf16, stepm, bn, grid, lds, st);
+    launch_meta<KIND, true>(a, scf16, stepm, variant, bn, grid, lds, st);
   else
-    launch_meta<KIND, false>(a, scf16, stepm, bn, grid, lds, st);
+    launch_meta<KIND, false>(a, scf16, stepm, variant, bn, grid, lds, st);
 }
 
 }  // namespace
@@ -436,14 +494,28 @@ size_t sglq_aop_bytes(const sglq_dev *d, int64_t Mpad, int split) {
   return (size_t)(split ? 2 : 1) * d->nsteps * 4 * Mpad * 16;
 }
 
+// Rows per workgroup of the dense GEMM.  (The 256-row prescaled variant, MB = 8, needs one
+// wave per SIMD and measured slower than two 128-row workgroups per CU; it stays instantiated
+// for tuning but is not selected.)
+int64_t sglq_gemm_rows(const sglq_dev *d, int split) {
+  (void)d;
+  (void)split;
+  return 128;
+}
+
 int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
                   const int *rowexp, int64_t M, int64_t Mpad, int64_t nblk, int split,
                   const float *bias, float *C, int64_t ldc, hipStream_t st) {
+  const bool direct = d->kind == SGLQ_KIND_E2M1 ||
+                      (d->prescale && d->meta_mode == SGLQ_META_GROUP);
+  // grouped row blocks hold at most 128 rows of one expert: 128-row tiles there
+  const int variant = !direct ? 0 : 1;
+  const int bmr = variant == 2 ? 256 : 128;
   // 128-column tiles unless that leaves the chip under-filled
   int bn = 128;
   if (nblk * ((d->N + 127) / 128) < 512 || d->meta_mode == SGLQ_META_STEP) bn = 64;
   const int nbn = (int)((d->N + bn - 1) / bn);
-  const size_t lds = (size_t)2 * (split ? 2 : 1) * d->spc * 4 * BM * 16;
+  const size_t lds = (size_t)2 * (split ? 2 : 1) * d->spc * 4 * bmr * 16;
   GemmArgs a;
   memset(&a, 0, sizeof(a));
   a.codes = d->codes;
@@ -474,13 +546,13 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
   const int stepm = d->meta_mode == SGLQ_META_STEP;
   switch (d->kind) {
     case SGLQ_KIND_U4:
-      launch_split<SGLQ_KIND_U4>(a, split, d->scf16, stepm, bn, grid, lds, st);
+      launch_split<SGLQ_KIND_U4>(a, split, d->scf16, stepm, variant, bn, grid, lds, st);
       break;
     case SGLQ_KIND_U8:
-      launch_split<SGLQ_KIND_U8>(a, split, d->scf16, stepm, bn, grid, lds, st);
+      launch_split<SGLQ_KIND_U8>(a, split, d->scf16, stepm, variant, bn, grid, lds, st);
       break;
     default:
-      launch_split<SGLQ_KIND_E2M1>(a, split, 1, 0, bn, grid, lds, st);
+      launch_split<SGLQ_KIND_E2M1>(a, split, 1, 0, variant, bn, grid, lds, st);
       break;
   }
   SGLQ_HIP(hipGetLastError());
@@ -492,12 +564,13 @@ fail:
 int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
               float *C, int64_t ldc, hipStream_t st) {
   const int split = dt == SGLQ_DT_F32;
-  const int64_t Mpad = (M + BM - 1) / BM * BM;
+  const int64_t bmr = sglq_gemm_rows(d, split);
+  const int64_t Mpad = (M + bmr - 1) / bmr * bmr;
   const size_t aop_bytes = sglq_aop_bytes(d, Mpad, split);
   if (sglq_ws_reserve(d, aop_bytes + (size_t)Mpad * sizeof(int) + 256) != 0) return -1;
   void *aop = d->ws;
   int *rowexp = (int *)((char *)d->ws + aop_bytes);
   if (sglq_prep_a(d, 0, A, dt, lda, M, Mpad, nullptr, 0, split, aop, rowexp, st) != 0)
     return -1;
-  return sglq_gemm_run(d, nullptr, aop, rowexp, M, Mpad, Mpad / BM, split, bias, C, ldc, st);
+  return sglq_gemm_run(d, nullptr, aop, rowexp, M, Mpad, Mpad / bmr, split, bias, C, ldc, st);
 }

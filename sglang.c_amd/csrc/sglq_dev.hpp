@@ -34,6 +34,7 @@ struct sglq_dev {
   int dev;
   int kind;       // SGLQ_KIND_*
   int scf16;      // U4/U8 meta entries hold f16 scales (4 B) rather than f32 (8 B)
+  int prescale;   // f16 scales with |s| in [2^-14, 128]: (q - z) * s is a normal f16 number
   int src;        // SGLQ_SRC_* it was built from
   int meta_mode;  // SGLQ_META_*
   int kident;     // kmap is the identity on [0, K) (no act-order, no padding inside K)
