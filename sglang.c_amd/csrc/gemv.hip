@@ -19,6 +19,8 @@
 // row by an exact power of two so it sits well inside f16 range; f32 inputs are split into f16
 // hi + lo parts (about 22 significant bits), bf16/f16 inputs fit one f16 part.  The power of
 // two is undone exactly on the result.
+#include <string.h>
+
 #include "sglq_dev.hpp"
 
 namespace {
@@ -34,6 +36,15 @@ struct GemvArgs {
   int *cnt;     // [ncg]
   int64_t lda, ldc;
   int N, K, M, adt, ntile, nchunk, nmeta, cpg, S, ncg, ks, tpg;
+  // grouped (MoE decode): blockIdx.y picks a row segment {expert, first row, rows, -} whose
+  // expert supplies the weights; rows are read as A row r (amode 0), A row rowmap[r] (amode 1)
+  // or silu(A[r][k]) * A[r][kcols + k] of an f32 A (amode 2); C row r is written
+  const int4 *segs;
+  const int *nseg;
+  const u32x4_t *const *codes_e;
+  const void *const *meta_e;
+  const int32_t *rowmap;
+  int amode, kcols;
 };
 
 __device__ __forceinline__ float bf16_bits(uint32_t b) { return __uint_as_float(b << 16); }
@@ -47,10 +58,24 @@ __device__ __forceinline__ float act1(const void *A, int dt, int64_t i) {
   return dt == SGLQ_DT_BF16 ? bf16_bits(b) : f16_bits(b);
 }
 
-// Activations of row m at device positions kp .. kp+7 (0 outside [0, K) and in padding), one
-// element at a time (the general path: act-order gather, unaligned rows, K % 8 != 0).
-__device__ __forceinline__ void load8(const GemvArgs &a, int m, int kp, float v[8]) {
-  const int64_t rb = (int64_t)m * a.lda;
+// Activations of source row `row` at device positions kp .. kp+7 (0 outside [0, K) and in
+// padding), one element at a time (the general path: act-order gather, unaligned rows,
+// K % 8 != 0, SwiGLU rows).
+__device__ __forceinline__ float swiglu_at(const GemvArgs &a, int64_t rb, int k) {
+  const float g = ((const float *)a.A)[rb + k];  // silu as reference src/deepseek.c:662-663
+  return (g / (1.0f + expf(-g))) * ((const float *)a.A)[rb + a.kcols + k];
+}
+
+__device__ __forceinline__ void load8(const GemvArgs &a, int64_t row, int kp, float v[8]) {
+  const int64_t rb = row * a.lda;
+  if (a.amode == 2) {
+#pragma unroll
+    for (int o = 0; o < 8; o++) {
+      const int k = a.kmap ? a.kmap[kp + o] : (kp + o < a.K ? kp + o : -1);
+      v[o] = k >= 0 ? swiglu_at(a, rb, k) : 0.f;
+    }
+    return;
+  }
   if (a.kmap == nullptr) {
 #pragma unroll
     for (int o = 0; o < 8; o++) v[o] = kp + o < a.K ? act1(a.A, a.adt, rb + kp + o) : 0.f;
@@ -153,7 +178,22 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   const int c0 = cw0 + ks * CPW;                  // first chunk of this wave
   const int ncw = min(a.ks * CPW, a.nchunk - cw0);  // chunks in the workgroup's range
   const int kp0 = cw0 * SPC * 32;
-  const int M = a.M;
+  int M = a.M, row0 = 0;
+  const u32x4_t *codes = a.codes;
+  const void *meta = a.meta;
+  if (a.segs) {
+    if ((int)blockIdx.y >= *a.nseg) return;
+    const int4 sg = a.segs[blockIdx.y];
+    row0 = sg.y;
+    M = sg.z;
+    codes = a.codes_e[sg.x];
+    meta = a.meta_e[sg.x];
+  }
+  // source row of activation row m (m < M)
+  auto src_row = [&](int m) -> int64_t {
+    const int r = row0 + m;
+    return a.amode == 1 ? (int64_t)a.rowmap[r] : (int64_t)r;
+  };
   const int IPR = a.ks * CPW * SPC * 4;           // 8-element activation items per row
   const int RS = IPR + 1;                         // LDS row stride (+1 spreads rows over banks)
   const int items = M * IPR;
@@ -177,7 +217,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
     const int kp = item_kp(r);
     x.ok = it < items && (r >> 2) < ncw * SPC && (!FAST || kp < a.K);
     if constexpr (FAST) {
-      const int64_t off = (int64_t)min(m, M - 1) * a.lda + (x.ok ? kp : 0);
+      const int64_t off = src_row(min(m, M - 1)) * a.lda + (x.ok ? kp : 0);
       const u32x4_t *p = (const u32x4_t *)((const char *)a.A + off * (SPLIT ? 4 : 2));
 #pragma unroll
       for (int i = 0; i < RW; i++) x.q[i] = p[i];
@@ -200,7 +240,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
       }
     } else {
       const int m = it / IPR;
-      load8(a, m, item_kp(it - m * IPR), v);
+      load8(a, src_row(m), item_kp(it - m * IPR), v);
     }
   };
   auto amax_item = [&](int it, const float (&v)[8]) {
@@ -237,15 +277,15 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   MT mv[NMV];
   const int64_t mrow = ((int64_t)tl * 16 + n16) * a.nmeta;
   if constexpr (E2M1) {
-    const uint32_t *ep = (const uint32_t *)((const uint8_t *)a.meta + mrow);
+    const uint32_t *ep = (const uint32_t *)((const uint8_t *)meta + mrow);
 #pragma unroll
     for (int i = 0; i < CPW; i++) mv[i] = ep[min(c0 + i, clast)];
   } else if constexpr (STEPM) {
-    const MT *mp = (const MT *)a.meta + mrow;
+    const MT *mp = (const MT *)meta + mrow;
 #pragma unroll
     for (int i = 0; i < CPW * SPC; i++) mv[i] = mp[min(c0 * SPC + i, clast * SPC + SPC - 1)];
   } else {
-    const MT *mp = (const MT *)a.meta + mrow;
+    const MT *mp = (const MT *)meta + mrow;
     const int cc = min(c0, clast);
     int g = cc / a.cpg, r = cc - g * a.cpg;
     const int glast = clast / a.cpg;
@@ -258,7 +298,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
       }
     }
   }
-  const u32x4_t *cp = a.codes + (int64_t)tl * a.nchunk * 64 + lane;
+  const u32x4_t *cp = codes + (int64_t)tl * a.nchunk * 64 + lane;
   u32x4_t wv[CPW];
 #pragma unroll
   for (int i = 0; i < CPW; i++) wv[i] = __builtin_nontemporal_load(cp + min(c0 + i, clast) * 64);
@@ -370,7 +410,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
       if (r < M) {
         const float v = ldexpf(acc[i], s_exp[r]);
         if (a.S == 1)
-          a.C[r * a.ldc + n] = v + (a.bias ? a.bias[n] : 0.f);
+          a.C[(int64_t)(row0 + r) * a.ldc + n] = v + (a.bias ? a.bias[n] : 0.f);
         else  // device-scope store: written through to the level all XCDs share
           __hip_atomic_store(&a.part[((int64_t)sidx * M + r) * a.N + n], v, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
@@ -430,7 +470,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 }
 
 template <int KIND, int CPW, bool SPLIT, bool FAST>
-void launch4(const GemvArgs &a, int scf16, int stepm, size_t lds, unsigned grid, unsigned nthr,
+void launch4(const GemvArgs &a, int scf16, int stepm, size_t lds, dim3 grid, unsigned nthr,
              hipStream_t st) {
   if constexpr (KIND == SGLQ_KIND_E2M1) {
     k_gemv<KIND, CPW, SPLIT, true, false, FAST><<<grid, nthr, lds, st>>>(a);
@@ -451,7 +491,7 @@ void launch4(const GemvArgs &a, int scf16, int stepm, size_t lds, unsigned grid,
 
 template <int KIND, int CPW>
 void launch_cpw(const GemvArgs &a, bool split, int scf16, int stepm, bool fast, size_t lds,
-                unsigned grid, unsigned nthr, hipStream_t st) {
+                dim3 grid, unsigned nthr, hipStream_t st) {
   if (split) {
     if (fast)
       launch4<KIND, CPW, true, true>(a, scf16, stepm, lds, grid, nthr, st);
@@ -467,7 +507,7 @@ void launch_cpw(const GemvArgs &a, bool split, int scf16, int stepm, bool fast, 
 
 template <int KIND>
 void launch_kind(const GemvArgs &a, int cpw, bool split, int scf16, int stepm, bool fast,
-                 size_t lds, unsigned grid, unsigned nthr, hipStream_t st) {
+                 size_t lds, dim3 grid, unsigned nthr, hipStream_t st) {
   switch (cpw) {
     case 4: launch_cpw<KIND, 4>(a, split, scf16, stepm, fast, lds, grid, nthr, st); break;
     case 12: launch_cpw<KIND, 12>(a, split, scf16, stepm, fast, lds, grid, nthr, st); break;
@@ -524,12 +564,12 @@ fail:
   return -1;
 }
 
-int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
-              float *C, int64_t ldc, hipStream_t st) {
-  const bool split = dt == SGLQ_DT_F32;
-  const Plan pl = plan_gemv(d, M, split);
-  const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
+namespace {
+
+GemvArgs base_args(const sglq_dev *d, const Plan &pl, const void *A, int dt, int64_t lda,
+                   int64_t M, const float *bias, float *C, int64_t ldc) {
   GemvArgs a;
+  memset(&a, 0, sizeof(a));
   a.codes = d->codes;
   a.meta = d->meta;
   a.A = A;
@@ -552,15 +592,14 @@ int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
   a.ncg = pl.ncg;
   a.ks = pl.ks;
   a.tpg = pl.tpg;
-  const bool fast = d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
-                    (lda * esz) % 16 == 0;
-  const unsigned grid = (unsigned)(pl.ncg * pl.S);
+  return a;
+}
+
+int launch_gemv(const sglq_dev *d, const GemvArgs &a, const Plan &pl, bool split, bool fast,
+                unsigned gy, hipStream_t st) {
+  const dim3 grid((unsigned)(pl.ncg * pl.S), gy);
   const unsigned nthr = (unsigned)(pl.ks * pl.tpg * 64);
   const int stepm = d->meta_mode == SGLQ_META_STEP;
-  if (pl.S > d->gv_split) {
-    sglq_log_error("qlinear: GEMV split %d exceeds its state (%d)", pl.S, d->gv_split);
-    return -1;
-  }
   switch (d->kind) {
     case SGLQ_KIND_U4:
       launch_kind<SGLQ_KIND_U4>(a, pl.cpw, split, d->scf16, stepm, fast, pl.lds, grid, nthr, st);
@@ -576,6 +615,51 @@ int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
   return 0;
 fail:
   return -1;
+}
+
+}  // namespace
+
+int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
+              float *C, int64_t ldc, hipStream_t st) {
+  const bool split = dt == SGLQ_DT_F32;
+  const Plan pl = plan_gemv(d, M, split);
+  const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
+  if (pl.S > d->gv_split) {
+    sglq_log_error("qlinear: GEMV split %d exceeds its state (%d)", pl.S, d->gv_split);
+    return -1;
+  }
+  const GemvArgs a = base_args(d, pl, A, dt, lda, M, bias, C, ldc);
+  const bool fast = d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
+                    (lda * esz) % 16 == 0;
+  return launch_gemv(d, a, pl, split, fast, 1, st);
+}
+
+int sglq_gemv_grouped_fits(const sglq_dev *d, int64_t max_rows, int split) {
+  return max_rows <= 16 && plan_gemv(d, max_rows, split).S == 1;
+}
+
+int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows,
+                      int64_t max_segs, const void *A, int dt, int64_t lda, int amode,
+                      const int32_t *rowmap, int kcols, float *C, int64_t ldc, hipStream_t st) {
+  const bool split = dt == SGLQ_DT_F32;
+  const Plan pl = plan_gemv(d, max_rows, split);
+  const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
+  if (pl.S != 1 || max_rows > 16) {
+    sglq_log_error("qlinear: grouped GEMV needs one K range per workgroup (rows %lld)",
+                   (long long)max_rows);
+    return -1;
+  }
+  GemvArgs a = base_args(d, pl, A, dt, lda, max_rows, nullptr, C, ldc);
+  a.segs = (const int4 *)grp->segs;
+  a.nseg = grp->nseg;
+  a.codes_e = (const u32x4_t *const *)grp->codes;
+  a.meta_e = grp->meta;
+  a.rowmap = rowmap;
+  a.amode = amode;
+  a.kcols = kcols;
+  const bool fast = amode != 2 && d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
+                    (lda * esz) % 16 == 0;
+  return launch_gemv(d, a, pl, split, fast, (unsigned)max_segs, st);
 }
 
 extern "C" int sglq_forward(sglq_dev *d, const void *A, int dt, int64_t M, const float *bias,

@@ -6,10 +6,12 @@
 //   k_moe_route   one workgroup: counts (token, slot) pairs per expert, orders them by expert
 //                 (inside an expert by pair index, so the order is deterministic), and writes
 //                 the row-block table of the grouped GEMMs (blocks of <= 128 rows of one expert)
-//   prep (gather) A operands of the expert-sorted rows of h
-//   grouped GEMM  gu = h_rows * Wgu[e]^T for every row block, each with its expert's weights
-//   prep (SwiGLU) A operands of silu(gu[:, :mi]) * gu[:, mi:]
-//   grouped GEMM  o = a * Wdn[e]^T
+//   prefill:  prep (gather) A operands of the expert-sorted rows of h
+//             grouped GEMM  gu = h_rows * Wgu[e]^T, each row block with its expert's weights
+//             prep (SwiGLU) A operands of silu(gu[:, :mi]) * gu[:, mi:]
+//             grouped GEMM  o = a * Wdn[e]^T
+//   decode (T <= 4): the same two products as grouped decode GEMVs that gather the token rows
+//             and form the SwiGLU rows while staging their activations
 //   k_moe_combine out[t] = sum_j w[t,j] * o[row of (t,j)], slots added in order j = 0..k-1
 #include <string.h>
 
@@ -191,22 +193,34 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
     float *o = (float *)(ws + o_o);
     k_moe_route<<<1, 1024, 0, st>>>(topk_ids, (int)P, k, n_exp, rowmap, pos, segs, nseg);
     SGLQ_HIP(hipGetLastError());
-    // rows of Mpad beyond P: rowmap entries are never read (prep zeroes rows >= M)
-    if (sglq_prep_a(g0, 1, h, h_dtype, E, P, Mpad, rowmap, 0, split1, ws + o_aop1,
-                    (int *)(ws + o_rexp1), st) != 0)
-      return -1;
     sglq_group g1 = {dp, dp + n_exp, (const uint8_t *const *)(dp + 2 * n_exp), segs, nseg};
-    if (sglq_gemm_run(g0, &g1, ws + o_aop1, (const int *)(ws + o_rexp1), P, Mpad, maxblk,
-                      split1, nullptr, gu, 2 * mi, st) != 0)
-      return -1;
-    if (sglq_prep_a(d0, 2, gu, SGLQ_DT_F32, 2 * mi, P, Mpad, nullptr, (int)mi, 1, ws + o_aop2,
-                    (int *)(ws + o_rexp2), st) != 0)
-      return -1;
     sglq_group g2 = {dp + 3 * n_exp, dp + 4 * n_exp, (const uint8_t *const *)(dp + 5 * n_exp),
                      segs, nseg};
-    if (sglq_gemm_run(d0, &g2, ws + o_aop2, (const int *)(ws + o_rexp2), P, Mpad, maxblk, 1,
-                      nullptr, o, E, st) != 0)
-      return -1;
+    // decode-sized batches (every expert has at most T <= 4 rows): grouped GEMVs that read the
+    // token rows and the SwiGLU rows directly; otherwise operand prep + grouped GEMMs
+    if (T <= 4 && sglq_gemv_grouped_fits(g0, T, split1) && sglq_gemv_grouped_fits(d0, T, 1)) {
+      const int64_t max_segs = P < n_exp ? P : n_exp;
+      if (sglq_gemv_grouped(g0, &g1, T, max_segs, h, h_dtype, E, 1, rowmap, 0, gu, 2 * mi,
+                            st) != 0)
+        return -1;
+      if (sglq_gemv_grouped(d0, &g2, T, max_segs, gu, SGLQ_DT_F32, 2 * mi, 2, nullptr, (int)mi,
+                            o, E, st) != 0)
+        return -1;
+    } else {
+      // rows of Mpad beyond P: rowmap entries are never read (prep zeroes rows >= M)
+      if (sglq_prep_a(g0, 1, h, h_dtype, E, P, Mpad, rowmap, 0, split1, ws + o_aop1,
+                      (int *)(ws + o_rexp1), st) != 0)
+        return -1;
+      if (sglq_gemm_run(g0, &g1, ws + o_aop1, (const int *)(ws + o_rexp1), P, Mpad, maxblk,
+                        split1, nullptr, gu, 2 * mi, st) != 0)
+        return -1;
+      if (sglq_prep_a(d0, 2, gu, SGLQ_DT_F32, 2 * mi, P, Mpad, nullptr, (int)mi, 1,
+                      ws + o_aop2, (int *)(ws + o_rexp2), st) != 0)
+        return -1;
+      if (sglq_gemm_run(d0, &g2, ws + o_aop2, (const int *)(ws + o_rexp2), P, Mpad, maxblk, 1,
+                        nullptr, o, E, st) != 0)
+        return -1;
+    }
     dim3 grid((unsigned)((E + 255) / 256), (unsigned)T);
     k_moe_combine<<<grid, 256, 0, st>>>(o, E, pos, topk_w, k, (int)E, out);
     SGLQ_HIP(hipGetLastError());

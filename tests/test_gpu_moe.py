@@ -60,6 +60,11 @@ def test_moe_unrouted_slots(orc):
     _check(orc, 6, 256, 256, 9, 3, seed=41, dtypes=("f32",), drop=True)
 
 
+def test_moe_decode_batch_f32(orc):
+    """Decode batches (T <= 4) take the grouped-GEMV path; f32 and bf16 tokens."""
+    _check(orc, 16, 512, 256, 3, 4, seed=51)
+
+
 def test_moe_decode_deepseek_shape(orc):
     """BASELINE config 5, decode: one token, 6 of 64 experts, hidden 2048, inter 1408."""
     _check(orc, 64, 2048, 1408, 1, 6, seed=0x5EED0005, dtypes=("bf16",))
