@@ -111,6 +111,7 @@ struct GemmArgs {
   float *C;
   int64_t ldc;
   int M, Mpad, N, ntile, nchunk, nsteps, nmeta, cpg, nbn;
+  int nbm, xmap;  // dense: row blocks; 1 = XCD-aware tile order (see k_gemm)
 };
 
 union H8 {
@@ -214,7 +215,26 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int wm = w & 1, wn = w >> 1;
   const int n16 = lane & 15, kq = lane >> 4;
-  const int bn = blockIdx.x % a.nbn, bm = blockIdx.x / a.nbn;
+  // Tile order.  Workgroup i runs on XCD i % 8, and each XCD has its own L2.  With xmap the
+  // row blocks are dealt to XCDs so that one XCD's workgroups share few activation row
+  // blocks (kept in its L2) while the weight columns stream through: nbm >= 8 gives XCD x the
+  // row blocks x, x+8, ...; nbm < 8 gives each row block 8/nbm XCDs that split the columns.
+  int bn, bm;
+  if (a.xmap) {
+    const int x = (int)(blockIdx.x & 7), l = (int)(blockIdx.x >> 3);
+    if (a.nbm >= 8) {
+      bm = x + 8 * (l / a.nbn);
+      bn = l % a.nbn;
+    } else {
+      const int r = 8 / a.nbm;
+      bm = x % a.nbm;
+      bn = x / a.nbm + r * l;
+    }
+    if (bm >= a.nbm || bn >= a.nbn) return;
+  } else {
+    bn = (int)(blockIdx.x % (unsigned)a.nbn);
+    bm = (int)(blockIdx.x / (unsigned)a.nbn);
+  }
   int m0 = bm * BMR, mend = a.M;
   const u32x4_t *codes = a.codes;
   const void *meta = a.meta;
@@ -265,17 +285,22 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   u32x4_t bw[TN];
   MT bm_[TN][NMV];
   int cref[TN];
-  auto load_b = [&](int c, int g) {
+  u32x4_t bw2[TN];
+  MT bm2[TN][NMV];
+  // weights of chunk c (clamped to the last chunk: valid memory, never used past the end)
+  auto load_b = [&](int c, u32x4_t (&w_)[TN], MT (&m_)[TN][NMV]) {
+    c = min(c, a.nchunk - 1);
+    const int g = c / a.cpg;
 #pragma unroll
     for (int j = 0; j < TN; j++) {
-      bw[j] = ldg_nt(bptr[j] + c * 64);
+      w_[j] = ldg_nt(bptr[j] + c * 64);
       if constexpr (E2M1) {
-        bm_[j][0] = ldg((const uint32_t *)mptr[j] + c);
+        m_[j][0] = ldg((const uint32_t *)mptr[j] + c);
       } else if constexpr (STEPM) {
 #pragma unroll
-        for (int s = 0; s < SPC; s++) bm_[j][s] = ldg(mptr[j] + c * SPC + s);
+        for (int s = 0; s < SPC; s++) m_[j][s] = ldg(mptr[j] + c * SPC + s);
       } else {
-        bm_[j][0] = ldg(mptr[j] + g);
+        m_[j][0] = ldg(mptr[j] + g);
       }
     }
   };
@@ -297,9 +322,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
       for (int j = 0; j < TN; j++) tmp[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
   }
 
-  int g = 0, gr = 0;  // group of the next chunk (META_GROUP), chunks into it
+  // weights are loaded two chunks ahead (HBM latency), activations one chunk ahead (L2)
   load_a(0);
-  load_b(0, 0);
+  load_b(0, bw, bm_);
+  load_b(1, bw2, bm2);
   store_a(0);
   __syncthreads();
   for (int c = 0; c < a.nchunk; c++) {
@@ -309,16 +335,16 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       cw[j] = bw[j];
+      bw[j] = bw2[j];
 #pragma unroll
-      for (int s = 0; s < NMV; s++) cm[j][s] = bm_[j][s];
-    }
-    if (++gr == a.cpg) {
-      gr = 0;
-      g++;
+      for (int s = 0; s < NMV; s++) {
+        cm[j][s] = bm_[j][s];
+        bm_[j][s] = bm2[j][s];
+      }
     }
     if (c + 1 < a.nchunk) {
       load_a(c + 1);
-      load_b(c + 1, g);
+      load_b(c + 2, bw2, bm2);
     }
     const half8_t *sa = s_a + buf * ITEMS + wm * (16 * MB) + n16;
     float sc[TN];
@@ -542,7 +568,14 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
   a.nmeta = (int)d->nmeta;
   a.cpg = d->cpg > 0 ? (int)d->cpg : 1;
   a.nbn = nbn;
-  const unsigned grid = (unsigned)(nblk * nbn);
+  a.nbm = (int)nblk;
+  unsigned grid = (unsigned)(nblk * nbn);
+  if (!grp && ((nblk >= 8 && nblk % 8 == 0) || (nblk < 8 && 8 % nblk == 0))) {
+    a.xmap = 1;
+    const int64_t per_xcd = nblk >= 8 ? (nblk / 8) * nbn : (nbn + 8 / nblk - 1) / (8 / nblk);
+    grid = (unsigned)(8 * per_xcd);
+  }
+
   const int stepm = d->meta_mode == SGLQ_META_STEP;
   switch (d->kind) {
     case SGLQ_KIND_U4:

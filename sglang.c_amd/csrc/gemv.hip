@@ -45,6 +45,7 @@ struct GemvArgs {
   const void *const *meta_e;
   const int32_t *rowmap;
   int amode, kcols;
+  uint32_t ipr_magic;  // ceil(2^32 / items per row)
 };
 
 __device__ __forceinline__ float bf16_bits(uint32_t b) { return __uint_as_float(b << 16); }
@@ -164,7 +165,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
   constexpr int NP = SPLIT ? 2 : 1;
   constexpr int RW = SPLIT ? 2 : 1;  // 128-bit words per 8-element activation item
-  constexpr int KEEP = 4;            // items per thread held in registers across the passes
+  constexpr int KEEP = 2;            // items per thread held in registers across the passes
   extern __shared__ half8_t s_act[];  // [NP][M][RS] activation operands, then [waves][64] acc
   __shared__ unsigned s_amax[16];
   __shared__ int s_exp[16];
@@ -190,10 +191,12 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
     meta = a.meta_e[sg.x];
   }
   // source row of activation row m (m < M)
-  auto src_row = [&](int m) -> int64_t {
+  auto src_row = [&](int m) -> uint32_t {
     const int r = row0 + m;
-    return a.amode == 1 ? (int64_t)a.rowmap[r] : (int64_t)r;
+    return a.amode == 1 ? (uint32_t)a.rowmap[r] : (uint32_t)r;
   };
+  // it / IPR for it < 2^16 as one multiply-high by the host's ceil(2^32 / IPR)
+  auto row_of = [&](int it) { return (int)__umulhi((uint32_t)it, a.ipr_magic); };
   const int IPR = a.ks * CPW * SPC * 4;           // 8-element activation items per row
   const int RS = IPR + 1;                         // LDS row stride (+1 spreads rows over banks)
   const int items = M * IPR;
@@ -213,11 +216,12 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   };
   auto item_kp = [&](int r) { return kp0 + (r >> 2) * 32 + (r & 3) * 8; };
   auto load_raw = [&](int it, Raw &x) {
-    const int m = it / IPR, r = it - m * IPR;
+    const int m = row_of(it), r = it - m * IPR;
     const int kp = item_kp(r);
     x.ok = it < items && (r >> 2) < ncw * SPC && (!FAST || kp < a.K);
     if constexpr (FAST) {
-      const int64_t off = src_row(min(m, M - 1)) * a.lda + (x.ok ? kp : 0);
+      // element offset in 32 bits (the host keeps the activation block under 2^31 elements)
+      const uint32_t off = src_row(min(m, M - 1)) * (uint32_t)a.lda + (x.ok ? kp : 0);
       const u32x4_t *p = (const u32x4_t *)((const char *)a.A + off * (SPLIT ? 4 : 2));
 #pragma unroll
       for (int i = 0; i < RW; i++) x.q[i] = p[i];
@@ -239,7 +243,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
         for (int o = 0; o < 8; o++) v[o] = f16_bits((x.q[0][o >> 1] >> (16 * (o & 1))) & 0xFFFFu);
       }
     } else {
-      const int m = it / IPR;
+      const int m = row_of(it);
       load8(a, src_row(m), item_kp(it - m * IPR), v);
     }
   };
@@ -247,10 +251,10 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
     float mx = 0.f;
 #pragma unroll
     for (int o = 0; o < 8; o++) mx = fmaxf(mx, fabsf(v[o]));
-    atomicMax(&s_amax[it / IPR], __float_as_uint(mx));
+    atomicMax(&s_amax[row_of(it)], __float_as_uint(mx));
   };
   auto store_item = [&](int it, const float (&v)[8]) {
-    const int m = it / IPR, r = it - m * IPR;
+    const int m = row_of(it), r = it - m * IPR;
     const int e = s_exp[m];
     half8_t hi, lo;
 #pragma unroll
@@ -350,7 +354,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
     }
   };
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
-  float4_t t0 = {0.f, 0.f, 0.f, 0.f};
+  float4_t pacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
   half8_t opc[SPC * NP], opn[SPC * NP];
   read_ops(0, opc);
 #pragma unroll
@@ -370,21 +374,23 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
         sc = live ? sc : 0.f;
       }
       const half8_t b = unpack<KIND>(wv[i], j, zA, zB);
-      t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[j], b, t0, 0, 0, 0);
+      // even and odd chunks accumulate in separate registers: two independent MFMA chains
+      float4_t &tc = pacc[i & 1];
+      tc = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[j], b, tc, 0, 0, 0);
       if constexpr (SPLIT)
-        t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[SPC + j], b, t0, 0, 0, 0);
+        tc = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[SPC + j], b, tc, 0, 0, 0);
       if constexpr (E2M1 || STEPM) {
         if constexpr (E2M1) {
           const uint32_t ex = (mv[i] >> (8 * j)) & 255u;
           sc = (ex == 255u || !live) ? 0.f : ldexpf(1.0f, (int)ex - 127);  // ref qweight.c:361
         }
-        acc += sc * t0;
-        t0 = (float4_t){0.f, 0.f, 0.f, 0.f};
+        acc += sc * tc;
+        tc = (float4_t){0.f, 0.f, 0.f, 0.f};
       }
     }
     if constexpr (!E2M1 && !STEPM) {
-      acc += sc * t0;
-      t0 = (float4_t){0.f, 0.f, 0.f, 0.f};
+      acc += sc * pacc[i & 1];
+      pacc[i & 1] = (float4_t){0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int q = 0; q < SPC * NP; q++) opc[q] = opn[q];
@@ -592,6 +598,8 @@ GemvArgs base_args(const sglq_dev *d, const Plan &pl, const void *A, int dt, int
   a.ncg = pl.ncg;
   a.ks = pl.ks;
   a.tpg = pl.tpg;
+  const uint64_t ipr = (uint64_t)pl.ks * pl.cpw * d->spc * 4;
+  a.ipr_magic = (uint32_t)(((1ull << 32) + ipr - 1) / ipr);
   return a;
 }
 
@@ -630,7 +638,7 @@ int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
   }
   const GemvArgs a = base_args(d, pl, A, dt, lda, M, bias, C, ldc);
   const bool fast = d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
-                    (lda * esz) % 16 == 0;
+                    (lda * esz) % 16 == 0 && M * lda < (1ll << 31);
   return launch_gemv(d, a, pl, split, fast, 1, st);
 }
 
@@ -639,8 +647,9 @@ int sglq_gemv_grouped_fits(const sglq_dev *d, int64_t max_rows, int split) {
 }
 
 int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows,
-                      int64_t max_segs, const void *A, int dt, int64_t lda, int amode,
-                      const int32_t *rowmap, int kcols, float *C, int64_t ldc, hipStream_t st) {
+                      int64_t max_segs, const void *A, int dt, int64_t a_rows, int64_t lda,
+                      int amode, const int32_t *rowmap, int kcols, float *C, int64_t ldc,
+                      hipStream_t st) {
   const bool split = dt == SGLQ_DT_F32;
   const Plan pl = plan_gemv(d, max_rows, split);
   const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
@@ -658,7 +667,7 @@ int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows
   a.amode = amode;
   a.kcols = kcols;
   const bool fast = amode != 2 && d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
-                    (lda * esz) % 16 == 0;
+                    (lda * esz) % 16 == 0 && a_rows * lda < (1ll << 31);
   return launch_gemv(d, a, pl, split, fast, (unsigned)max_segs, st);
 }
 

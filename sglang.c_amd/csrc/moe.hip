@@ -200,11 +200,11 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
     // token rows and the SwiGLU rows directly; otherwise operand prep + grouped GEMMs
     if (T <= 4 && sglq_gemv_grouped_fits(g0, T, split1) && sglq_gemv_grouped_fits(d0, T, 1)) {
       const int64_t max_segs = P < n_exp ? P : n_exp;
-      if (sglq_gemv_grouped(g0, &g1, T, max_segs, h, h_dtype, E, 1, rowmap, 0, gu, 2 * mi,
+      if (sglq_gemv_grouped(g0, &g1, T, max_segs, h, h_dtype, T, E, 1, rowmap, 0, gu, 2 * mi,
                             st) != 0)
         return -1;
-      if (sglq_gemv_grouped(d0, &g2, T, max_segs, gu, SGLQ_DT_F32, 2 * mi, 2, nullptr, (int)mi,
-                            o, E, st) != 0)
+      if (sglq_gemv_grouped(d0, &g2, T, max_segs, gu, SGLQ_DT_F32, P, 2 * mi, 2, nullptr,
+                            (int)mi, o, E, st) != 0)
         return -1;
     } else {
       // rows of Mpad beyond P: rowmap entries are never read (prep zeroes rows >= M)

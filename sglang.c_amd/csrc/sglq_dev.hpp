@@ -111,12 +111,13 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop, con
                   int64_t ldc, hipStream_t st);
 // Grouped decode GEMV (MoE): one launch over the row segments of grp (each <= max_rows rows of
 // one expert, at most max_segs of them), activation rows per amode (0 A row r, 1 A row
-// rowmap[r], 2 silu(A[r][k]) * A[r][kcols + k] with f32 A).  Only when every workgroup can take
+// rowmap[r], 2 silu(A[r][k]) * A[r][kcols + k] with f32 A; A has a_rows rows).  Only when every workgroup can take
 // all of K (sglq_gemv_grouped_fits).
 int sglq_gemv_grouped_fits(const sglq_dev *d, int64_t max_rows, int split);
 int sglq_gemv_grouped(const sglq_dev *d, const struct sglq_group *grp, int64_t max_rows,
-                      int64_t max_segs, const void *A, int dt, int64_t lda, int amode,
-                      const int32_t *rowmap, int kcols, float *C, int64_t ldc, hipStream_t st);
+                      int64_t max_segs, const void *A, int dt, int64_t a_rows, int64_t lda,
+                      int amode, const int32_t *rowmap, int kcols, float *C, int64_t ldc,
+                      hipStream_t st);
 // Picks the decode GEMV split for a freshly built weight and allocates its state.
 int sglq_gemv_setup(sglq_dev *d);
 
