@@ -31,61 +31,146 @@ __device__ __forceinline__ float act_at(const void *A, int dt, int64_t i) {
 
 __device__ __forceinline__ constexpr int kofs4(int i) { return (i >> 1) + 4 * (i & 1); }
 
-// One workgroup (256 threads) per row of Aop (Mpad rows).  Source row of Aop row m:
+// A operands for the GEMM, in two launches.  Source row of Aop row m:
 //   MODE 0  A[m]                           (dense)
 //   MODE 1  A[rowmap[m]], zero if < 0       (MoE: token of each expert-sorted row)
 //   MODE 2  a_k = silu(A[m][k]) * A[m][kcols + k], A f32 (MoE: SwiGLU of the gate/up product,
 //           silu(g) = g / (1 + expf(-g)) as reference src/deepseek.c:662-663)
+// k_rowexp: one wave per row finds its largest |a| and the exact power of two that puts it in
+// [2^13, 2^14).  k_prep_a: workgroups of 16 rows x 64 items write the scaled f16 operands with
+// consecutive threads on consecutive rows of one 16-B item (Aop keeps the rows of an item
+// contiguous, so the stores coalesce).  vec: identity kmap with 16-byte aligned rows (8
+// elements load as one or two 128-bit loads).
+template <int MODE>
+__device__ __forceinline__ int64_t prep_src(const int32_t *rowmap, int M, int m) {
+  if (m >= M) return -1;
+  if constexpr (MODE == 1) return rowmap[m];
+  return m;
+}
+
+template <int MODE>
+__device__ __forceinline__ float prep_value(const void *A, int dt, int64_t rb, int kcols, int k) {
+  if constexpr (MODE == 2) {
+    const float g = ((const float *)A)[rb + k];
+    return (g / (1.0f + expf(-g))) * ((const float *)A)[rb + kcols + k];
+  } else {
+    return act_at(A, dt, rb + k);
+  }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void k_rowexp(const void *__restrict__ A, int dt, int64_t lda,
+                                                int M, int Mpad, int K, int nsteps,
+                                                const int32_t *__restrict__ kmap,
+                                                const int32_t *__restrict__ rowmap, int kcols,
+                                                int vec, int *__restrict__ rowexp) {
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (m >= Mpad) return;
+  const int64_t src = prep_src<MODE>(rowmap, M, m);
+  float mx = 0.f;
+  if (src >= 0) {
+    const int64_t rb = src * lda;
+    if (MODE != 2 && vec) {
+      // 8 elements per lane per 128-bit load, eight loads in flight at a time
+      const int nv = K / 8;
+      for (int v0 = 0; v0 < nv; v0 += 512) {
+        uint4 raw[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int vi = min(v0 + lane + 64 * j, nv - 1);
+          raw[j] = dt == SGLQ_DT_F32 ? *(const uint4 *)((const float *)A + rb + vi * 8)
+                                     : *(const uint4 *)((const uint16_t *)A + rb + vi * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          if (v0 + lane + 64 * j >= nv) continue;
+          const uint32_t wd[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+          if (dt == SGLQ_DT_F32) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) mx = fmaxf(mx, fabsf(__uint_as_float(wd[i])));
+            const uint4 hi4 = *(const uint4 *)((const float *)A + rb + (v0 + lane + 64 * j) * 8 + 4);
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(__uint_as_float(hi4.x)), fabsf(__uint_as_float(hi4.y))),
+                                 fmaxf(fabsf(__uint_as_float(hi4.z)), fabsf(__uint_as_float(hi4.w)))));
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+              const uint32_t hb = (wd[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+              const float x = dt == SGLQ_DT_BF16 ? __uint_as_float(hb << 16)
+                                                 : (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
+              mx = fmaxf(mx, fabsf(x));
+            }
+          }
+        }
+      }
+      for (int k = nv * 8 + lane; k < K; k += 64) mx = fmaxf(mx, fabsf(act_at(A, dt, rb + k)));
+    } else {
+      for (int kp = lane; kp < nsteps * 32; kp += 64) {
+        const int k = kmap ? kmap[kp] : (kp < K ? kp : -1);
+        if (k >= 0) mx = fmaxf(mx, fabsf(prep_value<MODE>(A, dt, rb, kcols, k)));
+      }
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) rowexp[m] = (mx > 0.f && mx <= 3.0e38f) ? ilogbf(mx) - 13 : 0;
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256) void k_prep_a(const void *__restrict__ A, int dt, int64_t lda,
                                                 int M, int Mpad, int K, int nsteps,
                                                 const int32_t *__restrict__ kmap,
                                                 const int32_t *__restrict__ rowmap, int kcols,
-                                                int perm4, int split, half8_t *__restrict__ aop,
-                                                int *__restrict__ rowexp) {
-  const int m = blockIdx.x;
-  const int tid = threadIdx.x;
-  __shared__ float red[4];
-  const int kp_n = nsteps * 32;
-  const int64_t plane = (int64_t)nsteps * 4 * Mpad;  // 16-B items per piece
-  int64_t src = m;
-  if constexpr (MODE == 1) src = m < M ? rowmap[m] : -1;
-  if (m >= M || src < 0) {
-    const half8_t z = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int it = tid; it < nsteps * 4; it += 256) {
-      aop[(int64_t)it * Mpad + m] = z;
-      if (split) aop[plane + (int64_t)it * Mpad + m] = z;
-    }
-    if (tid == 0) rowexp[m] = 0;
-    return;
-  }
-  const int64_t rb = src * lda;
-  auto value = [&](int k) -> float {
-    if constexpr (MODE == 2) {
-      const float g = ((const float *)A)[rb + k];
-      return (g / (1.0f + expf(-g))) * ((const float *)A)[rb + kcols + k];
+                                                int perm4, int split, int vec,
+                                                half8_t *__restrict__ aop,
+                                                const int *__restrict__ rowexp) {
+  const int nitems = nsteps * 4;  // it = step * 4 + kq
+  const int64_t plane = (int64_t)nitems * Mpad;  // 16-B items per piece
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int u = threadIdx.x + 256 * q;
+    const int r = u & 15, it = blockIdx.y * 64 + (u >> 4);
+    const int m = blockIdx.x * 16 + r;
+    if (it >= nitems) continue;
+    const int64_t src = prep_src<MODE>(rowmap, M, m);
+    const int e = rowexp[m];
+    float v[8];
+    if (src < 0) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[i] = 0.f;
     } else {
-      return act_at(A, dt, rb + k);
+      const int64_t rb = src * lda;
+      const int kb = it * 8;
+      if (MODE != 2 && vec && kb + 8 <= K) {
+        float raw[8];
+        if (dt == SGLQ_DT_F32) {
+          const float4 *p = (const float4 *)((const float *)A + rb + kb);
+          const float4 x = p[0], y = p[1];
+          raw[0] = x.x; raw[1] = x.y; raw[2] = x.z; raw[3] = x.w;
+          raw[4] = y.x; raw[5] = y.y; raw[6] = y.z; raw[7] = y.w;
+        } else {
+          const uint4 x = *(const uint4 *)((const uint16_t *)A + rb + kb);
+          const uint32_t wd[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+          for (int i = 0; i < 8; i++) {
+            const uint32_t hb = (wd[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+            raw[i] = dt == SGLQ_DT_BF16 ? __uint_as_float(hb << 16)
+                                        : (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = raw[perm4 ? kofs4(i) : i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const int kp = kb + (perm4 ? kofs4(i) : i);
+          const int k = kmap ? kmap[kp] : (kp < K ? kp : -1);
+          v[i] = k >= 0 ? prep_value<MODE>(A, dt, rb, kcols, k) : 0.f;
+        }
+      }
     }
-  };
-  float mx = 0.f;
-  for (int kp = tid; kp < kp_n; kp += 256) {
-    const int k = kmap ? kmap[kp] : (kp < K ? kp : -1);
-    if (k >= 0) mx = fmaxf(mx, fabsf(value(k)));
-  }
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  if ((tid & 63) == 0) red[tid >> 6] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const int e = (mx > 0.f && mx <= 3.0e38f) ? ilogbf(mx) - 13 : 0;
-  if (tid == 0) rowexp[m] = e;
-  for (int it = tid; it < nsteps * 4; it += 256) {  // it = step * 4 + kq
     half8_t hi, lo;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const int kp = it * 8 + (perm4 ? kofs4(i) : i);
-      const int k = kmap ? kmap[kp] : (kp < K ? kp : -1);
-      const float x = k >= 0 ? ldexpf(value(k), -e) : 0.f;
+      const float x = ldexpf(v[i], -e);
       const _Float16 h = (_Float16)x;
       hi[i] = h;
       lo[i] = (_Float16)(x - (float)h);
@@ -112,6 +197,7 @@ struct GemmArgs {
   int64_t ldc;
   int M, Mpad, N, ntile, nchunk, nsteps, nmeta, cpg, nbn;
   int nbm, xmap;  // dense: row blocks; 1 = XCD-aware tile order (see k_gemm)
+  float *part;    // k_gemm_lds split over K: unscaled partial sums [gridDim.y][M][N], else null
 };
 
 union H8 {
@@ -436,6 +522,277 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   }
 }
 
+// Prefill GEMM with the weight tile dequantized once per workgroup into LDS (the "direct"
+// formats: prescaled U4/U8 groups and MXFP4).  128 x BN tile, 4 waves (2 x 2, each 64 x BN/2),
+// pipelined over stages of two MFMA steps: while the MFMAs of stage s read the A operands and
+// the f16 weights of stage s from one LDS buffer, the global loads of stage s + 1 are in flight;
+// their codes are then unpacked (each code once per workgroup, not once per wave) into the other
+// buffer.  LDS per workgroup: 2 x (16 KiB per A piece + BN/16 x 2 KiB), so two workgroups
+// share a CU.
+template <int KIND, int NP, int BN, int SSX, int WMW>
+__global__ __launch_bounds__(128 * WMW) void k_gemm_lds(GemmArgs a) {
+  constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
+  constexpr int SS = SSX < SPC ? SSX : SPC;  // MFMA steps per stage
+  constexpr int HPC = SPC / SS;         // stages per chunk
+  constexpr int NTH = 128 * WMW;        // threads: WMW waves along M x 2 along N
+  constexpr int BMR = 64 * WMW;
+  constexpr int NT16 = BN / 16;         // weight tiles per workgroup
+  constexpr int TN = NT16 / 2;          // per wave
+  constexpr int MB = 4;
+  constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
+  constexpr int AITEMS = NP * SS * 4 * BMR;  // 16-B A items per stage
+  constexpr int AIPT = AITEMS / NTH;
+  constexpr int BITEMS = NT16 * SS * 64;     // 16-B weight operands per stage
+  constexpr int PB = NT16 * 64 / NTH;        // (tile, lane) code words per thread
+  extern __shared__ half8_t s_lds[];         // [2][AITEMS] A, then [2][BITEMS] B
+  half8_t *s_a = s_lds;
+  half8_t *s_b = s_lds + 2 * AITEMS;
+
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int wm = w % WMW, wn = w / WMW;
+  const int n16 = lane & 15, kq = lane >> 4;
+  int bn, bm;
+  if (a.xmap) {
+    const int x = (int)(blockIdx.x & 7), l = (int)(blockIdx.x >> 3);
+    if (a.nbm >= 8) {
+      bm = x + 8 * (l / a.nbn);
+      bn = l % a.nbn;
+    } else {
+      const int r = 8 / a.nbm;
+      bm = x % a.nbm;
+      bn = x / a.nbm + r * l;
+    }
+    if (bm >= a.nbm || bn >= a.nbn) return;
+  } else {
+    bn = (int)(blockIdx.x % (unsigned)a.nbn);
+    bm = (int)(blockIdx.x / (unsigned)a.nbn);
+  }
+  int m0 = bm * BMR, mend = a.M;
+  const u32x4_t *codes = a.codes;
+  const void *meta = a.meta;
+  const uint8_t *colexp = a.colexp;
+  if (a.segs) {  // grouped: row block bm of the expert-sorted rows
+    if (bm >= *a.nseg) return;
+    const int4 sg = a.segs[bm];
+    m0 = sg.y;
+    mend = sg.y + sg.z;
+    codes = a.codes_e[sg.x];
+    meta = a.meta_e[sg.x];
+    if constexpr (E2M1) colexp = a.colexp_e[sg.x];
+  }
+  // split over K (blockIdx.y): this workgroup's stages [st0, st1)
+  const int nstage = a.nsteps / SS;
+  const int st0 = (int)((int64_t)nstage * blockIdx.y / gridDim.y);
+  const int st1 = (int)((int64_t)nstage * (blockIdx.y + 1) / gridDim.y);
+
+  // ---- activations: item q of this thread is row tid % BMR, slot r = RPI q + tid / BMR with
+  // r = (p * SS + s) * 4 + kq'
+  constexpr int RPI = NTH / BMR;  // 2
+  const int64_t plane = (int64_t)a.nsteps * 4 * a.Mpad;
+  const half8_t *abase = a.aop + m0 + (tid % BMR) + (int64_t)(tid / BMR) * a.Mpad;
+  half8_t areg[AIPT];
+  auto load_a = [&](int st) {
+#pragma unroll
+    for (int q = 0; q < AIPT; q++) {
+      const int r = RPI * q;  // + tid / BMR (in abase)
+      const int p = r / (SS * 4), sj = r % (SS * 4);
+      areg[q] = ldg(abase + p * plane + ((int64_t)st * SS * 4 + sj) * a.Mpad);
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < AIPT; q++) s_a[buf * AITEMS + tid + NTH * q] = areg[q];
+  };
+
+  // ---- weights: thread handles (tile tb, lane lb) = (p / 64, p % 64) for p = tid + 256 q
+  using MT = typename std::conditional<E2M1, uint32_t, uint32_t>::type;  // f16 scale | zero
+  const u32x4_t *bsrc[PB];
+  const uint32_t *msrc[PB];
+  int cref[PB];
+#pragma unroll
+  for (int q = 0; q < PB; q++) {
+    const int pp = tid + NTH * q, tb = pp >> 6, lb = pp & 63;
+    const int t = min(bn * NT16 + tb, a.ntile - 1);
+    bsrc[q] = codes + (int64_t)t * a.nchunk * 64 + lb;
+    msrc[q] = (const uint32_t *)((const char *)meta +
+                                 ((int64_t)t * 16 + (lb & 15)) * a.nmeta * (E2M1 ? 1 : 4));
+    if constexpr (E2M1) cref[q] = colexp[t * 16 + (lb & 15)];
+  }
+  u32x4_t breg[PB];
+  MT mreg[PB];
+  auto load_b = [&](int st) {
+    const int c = st / HPC, h = st % HPC;
+    const int g = c / a.cpg;
+#pragma unroll
+    for (int q = 0; q < PB; q++) {
+      if constexpr (KIND == SGLQ_KIND_U8) {
+        breg[q] = ldg_nt(bsrc[q] + c * 64);
+      } else if constexpr (SS == SPC) {
+        breg[q] = ldg_nt(bsrc[q] + c * 64);
+      } else {  // the two words of this half chunk
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        const u32x2_t x = ldg((const u32x2_t *)((const uint32_t *)(bsrc[q] + c * 64) + 2 * h));
+        breg[q] = (u32x4_t){x[0], x[1], 0u, 0u};
+      }
+      if constexpr (E2M1)
+        mreg[q] = ldg(msrc[q] + c) >> (8 * SS * h);  // e8m0 bytes of the stage's steps
+      else
+        mreg[q] = ldg(msrc[q] + g);
+    }
+  };
+  auto store_b = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < PB; q++) {
+      const int pp = tid + NTH * q, tb = pp >> 6, lb = pp & 63;
+      float sc;
+      half2_t zA = {0, 0}, zB = {0, 0}, s2 = {0, 0};
+      if constexpr (!E2M1) {
+        decode_meta<true>(mreg[q], sc, zA, zB);
+        const _Float16 hs = (_Float16)sc;
+        s2 = (half2_t){hs, hs};
+      }
+#pragma unroll
+      for (int s = 0; s < SS; s++) {
+        float fsc = 1.f;
+        if constexpr (E2M1) fsc = e8m0_rel((mreg[q] >> (8 * s)) & 255u, cref[q]);
+        H8 u;
+        u.v = unpack_b<KIND>(breg[q], s, zA, zB, fsc);
+        if constexpr (!E2M1) {
+#pragma unroll
+          for (int hh = 0; hh < 4; hh++) u.h[hh] = u.h[hh] * s2;
+        }
+        s_b[buf * BITEMS + (tb * SS + s) * 64 + lb] = u.v;
+      }
+    }
+  };
+
+  float4_t acc[MB][TN];
+#pragma unroll
+  for (int i = 0; i < MB; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) acc[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+  load_a(st0);
+  load_b(st0);
+  store_a(0);
+  store_b(0);
+  __syncthreads();
+  for (int st = st0; st < st1; st++) {
+    const int buf = (st - st0) & 1;
+    const bool more = st + 1 < st1;
+    if (more) {
+      load_a(st + 1);
+      load_b(st + 1);
+    }
+    const half8_t *sa = s_a + buf * AITEMS + wm * 64 + n16;
+    const half8_t *sb = s_b + buf * BITEMS + wn * TN * SS * 64 + lane;
+#pragma unroll
+    for (int s = 0; s < SS; s++) {
+      half8_t bv[TN];
+#pragma unroll
+      for (int j = 0; j < TN; j++) bv[j] = sb[(j * SS + s) * 64];
+#pragma unroll
+      for (int i = 0; i < MB; i++) {
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+          const half8_t av = sa[((p * SS + s) * 4 + kq) * BMR + i * 16];
+#pragma unroll
+          for (int j = 0; j < TN; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[j], acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+    if (more) {
+      store_a(buf ^ 1);
+      store_b(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // epilogue: lane holds rows 4*kq + r of each 16-row block, column n16 of each tile
+  const int t0 = bn * NT16 + wn * TN;
+  if (a.part) {  // split over K: raw partial sums, scaled by k_splitk_reduce
+    float *pp = a.part + (int64_t)blockIdx.y * a.M * a.N;
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int n = (t0 + j) * 16 + n16;
+      if (n >= a.N) continue;
+#pragma unroll
+      for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int m = m0 + wm * 64 + i * 16 + 4 * kq + r;
+          if (m < mend) pp[(int64_t)m * a.N + n] = acc[i][j][r];
+        }
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const int n = (t0 + j) * 16 + n16;
+    if (n >= a.N) continue;
+    const float bv = a.bias ? a.bias[n] : 0.f;
+    const int ce = E2M1 ? (int)colexp[min(t0 + j, a.ntile - 1) * 16 + n16] - 127 : 0;
+#pragma unroll
+    for (int i = 0; i < MB; i++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int m = m0 + wm * 64 + i * 16 + 4 * kq + r;
+        if (m < mend) a.C[(int64_t)m * a.ldc + n] = ldexpf(acc[i][j][r], a.rowexp[m] + ce) + bv;
+      }
+    }
+  }
+}
+
+// Sum of the K-split partials of k_gemm_lds in slice order (deterministic), then the row and
+// column exponents and the bias: C[m][n] = 2^(rowexp[m] + ce[n]) * sum_z part[z][m][n] + bias[n]
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ part, int nz,
+                                                       int M, int N,
+                                                       const int *__restrict__ rowexp,
+                                                       const uint8_t *__restrict__ colexp,
+                                                       const float *__restrict__ bias,
+                                                       float *__restrict__ C, int64_t ldc) {
+  const int n = (int)(blockIdx.x * 256 + threadIdx.x), m = (int)blockIdx.y;
+  if (n >= N) return;
+  const int64_t plane = (int64_t)M * N, o = (int64_t)m * N + n;
+  float s = part[o];
+  for (int z = 1; z < nz; z++) s += part[z * plane + o];
+  const int ce = colexp ? (int)colexp[n] - 127 : 0;
+  C[(int64_t)m * ldc + n] = ldexpf(s, rowexp[m] + ce) + (bias ? bias[n] : 0.f);
+}
+
+template <int KIND, int NP, int BN, int SSX, int WMW>
+void launch_lds1(const GemmArgs &a, dim3 grid, size_t lds, hipStream_t st) {
+  static bool raised = false;
+  auto f = k_gemm_lds<KIND, NP, BN, SSX, WMW>;
+  if (!raised)
+    raised = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 160 * 1024) == hipSuccess;
+  f<<<grid, 128 * WMW, lds, st>>>(a);
+}
+
+// LDS bytes of k_gemm_lds<.., BN, SSX, WMW>
+size_t lds_bytes(int spc, int np, int bn, int ssx, int wmw) {
+  const int ss = ssx < spc ? ssx : spc;
+  return (size_t)2 * (np * ss * 4 * 64 * wmw * 16 + (bn / 16) * ss * 64 * 16);
+}
+
+// tile configurations of k_gemm_lds: rows x columns per workgroup
+enum { LDS_128x128 = 0, LDS_128x64 = 1, LDS_256x128 = 2, LDS_64x128 = 3 };
+int lds_rows(int cfg) { return cfg == LDS_256x128 ? 256 : cfg == LDS_64x128 ? 64 : 128; }
+int lds_cols(int cfg) { return cfg == LDS_128x64 ? 64 : 128; }
+
+template <int KIND, int NP>
+void launch_lds(const GemmArgs &a, int cfg, dim3 grid, hipStream_t st) {
+  const int spc = KIND == SGLQ_KIND_U8 ? 2 : 4;
+  switch (cfg) {
+    case LDS_128x64: launch_lds1<KIND, NP, 64, 2, 2>(a, grid, lds_bytes(spc, NP, 64, 2, 2), st); break;
+    case LDS_256x128: launch_lds1<KIND, NP, 128, 2, 4>(a, grid, lds_bytes(spc, NP, 128, 2, 4), st); break;
+    case LDS_64x128: launch_lds1<KIND, NP, 128, 2, 1>(a, grid, lds_bytes(spc, NP, 128, 2, 1), st); break;
+    default: launch_lds1<KIND, NP, 128, 2, 2>(a, grid, lds_bytes(spc, NP, 128, 2, 2), st); break;
+  }
+}
+
 template <int KIND, bool SPLIT, bool SCF16, bool STEPM, bool PS, int MB>
 void launch_bn(const GemmArgs &a, int bn, unsigned grid, size_t lds, hipStream_t st) {
   // LDS beyond 64 KiB must be enabled per kernel once (160 KiB on gfx950)
@@ -499,16 +856,23 @@ int sglq_prep_a(const sglq_dev *d, int mode, const void *A, int dt, int64_t lda,
                 int *rowexp, hipStream_t st) {
   const int32_t *kmap = d->kident ? nullptr : d->kmap;
   const int perm4 = d->kind == SGLQ_KIND_U4;
-#define SGLQ_PREP(MODE)                                                                     \
-  k_prep_a<MODE><<<(unsigned)Mpad, 256, 0, st>>>(A, dt, lda, (int)M, (int)Mpad, (int)d->K,   \
-                                                  (int)d->nsteps, kmap, rowmap, kcols, perm4, \
-                                                  split, (half8_t *)aop, rowexp)
-  if (mode == 0)
+  const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
+  const int vec = kmap == nullptr && (uintptr_t)A % 16 == 0 && (lda * esz) % 16 == 0;
+  const dim3 pgrid((unsigned)(Mpad / 16), (unsigned)((d->nsteps * 4 + 63) / 64));
+#define SGLQ_PREP(MODE)                                                                         \
+  k_rowexp<MODE><<<(unsigned)((Mpad + 3) / 4), 256, 0, st>>>(A, dt, lda, (int)M, (int)Mpad,       \
+                                                             (int)d->K, (int)d->nsteps, kmap,     \
+                                                             rowmap, kcols, vec, rowexp);              \
+  k_prep_a<MODE><<<pgrid, 256, 0, st>>>(A, dt, lda, (int)M, (int)Mpad, (int)d->K, (int)d->nsteps, \
+                                        kmap, rowmap, kcols, perm4, split, vec, (half8_t *)aop,   \
+                                        rowexp)
+  if (mode == 0) {
     SGLQ_PREP(0);
-  else if (mode == 1)
+  } else if (mode == 1) {
     SGLQ_PREP(1);
-  else
+  } else {
     SGLQ_PREP(2);
+  }
 #undef SGLQ_PREP
   SGLQ_HIP(hipGetLastError());
   return 0;
@@ -523,6 +887,33 @@ size_t sglq_aop_bytes(const sglq_dev *d, int64_t Mpad, int split) {
 // Rows per workgroup of the dense GEMM.  (The 256-row prescaled variant, MB = 8, needs one
 // wave per SIMD and measured slower than two 128-row workgroups per CU; it stays instantiated
 // for tuning but is not selected.)
+// weights the LDS-dequant kernel takes: MXFP4, and groups whose f16 scales prescale the codes
+static bool lds_direct(const sglq_dev *d) {
+  const bool direct = d->kind == SGLQ_KIND_E2M1 ||
+                      (d->prescale && d->meta_mode == SGLQ_META_GROUP);
+  return direct && (d->kind == SGLQ_KIND_E2M1 || d->scf16);
+}
+
+// k_gemm_lds tiling of a dense call: 64 x 128 tiles for M <= 64, 128 x 64 below M = 1024, then
+// 256 x 128; and a split over K (deterministic, reduced in slice order) when the tiles alone
+// leave the 256 CUs under one workgroup each.  Every slice keeps at least 8 stages.
+struct LdsPlan {
+  int cfg, nz;
+};
+static LdsPlan lds_plan(const sglq_dev *d, int64_t M) {
+  LdsPlan p;
+  p.cfg = M <= 64 ? LDS_64x128 : M >= 1024 ? LDS_256x128 : LDS_128x64;
+  const int64_t tiles = (M + lds_rows(p.cfg) - 1) / lds_rows(p.cfg) *
+                        ((d->N + lds_cols(p.cfg) - 1) / lds_cols(p.cfg));
+  const int64_t nstage = d->nsteps / 2;
+  p.nz = 1;
+  if (tiles < 256) {
+    p.nz = (int)std::min<int64_t>((512 + tiles - 1) / tiles, std::min<int64_t>(16, nstage / 8));
+    if (p.nz < 1) p.nz = 1;
+  }
+  return p;
+}
+
 int64_t sglq_gemm_rows(const sglq_dev *d, int split) {
   (void)d;
   (void)split;
@@ -531,7 +922,7 @@ int64_t sglq_gemm_rows(const sglq_dev *d, int split) {
 
 int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
                   const int *rowexp, int64_t M, int64_t Mpad, int64_t nblk, int split,
-                  const float *bias, float *C, int64_t ldc, hipStream_t st) {
+                  const float *bias, float *C, int64_t ldc, float *part, hipStream_t st) {
   const bool direct = d->kind == SGLQ_KIND_E2M1 ||
                       (d->prescale && d->meta_mode == SGLQ_META_GROUP);
   // grouped row blocks hold at most 128 rows of one expert: 128-row tiles there
@@ -577,6 +968,50 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
   }
 
   const int stepm = d->meta_mode == SGLQ_META_STEP;
+  // direct formats with f16-exact scales: the LDS-dequant kernel
+  if (lds_direct(d)) {
+    const LdsPlan pl = grp ? LdsPlan{bn == 64 ? LDS_128x64 : LDS_128x128, 1} : lds_plan(d, M);
+    if (pl.nz > 1 && !part) {
+      sglq_log_error("prefill GEMM: no workspace for the split over K");
+      return -1;
+    }
+    const int cbm = lds_rows(pl.cfg), cbn = lds_cols(pl.cfg);
+    // grouped: row blocks of one expert each (at most 128 rows); dense: the rows of M
+    const int64_t nbm2 = grp ? nblk : (M + cbm - 1) / cbm;
+    a.nbn = (int)((d->N + cbn - 1) / cbn);
+    a.nbm = (int)nbm2;
+    a.xmap = 0;
+    a.part = pl.nz > 1 ? part : nullptr;
+    unsigned gx = (unsigned)(nbm2 * a.nbn);
+    if (!grp && ((nbm2 >= 8 && nbm2 % 8 == 0) || (nbm2 < 8 && 8 % nbm2 == 0))) {
+      a.xmap = 1;
+      const int64_t per = nbm2 >= 8 ? (nbm2 / 8) * a.nbn : (a.nbn + 8 / nbm2 - 1) / (8 / nbm2);
+      gx = (unsigned)(8 * per);
+    }
+    const dim3 grid2(gx, (unsigned)pl.nz);
+    switch (d->kind) {
+      case SGLQ_KIND_U4:
+        if (split) launch_lds<SGLQ_KIND_U4, 2>(a, pl.cfg, grid2, st);
+        else launch_lds<SGLQ_KIND_U4, 1>(a, pl.cfg, grid2, st);
+        break;
+      case SGLQ_KIND_U8:
+        if (split) launch_lds<SGLQ_KIND_U8, 2>(a, pl.cfg, grid2, st);
+        else launch_lds<SGLQ_KIND_U8, 1>(a, pl.cfg, grid2, st);
+        break;
+      default:
+        if (split) launch_lds<SGLQ_KIND_E2M1, 2>(a, pl.cfg, grid2, st);
+        else launch_lds<SGLQ_KIND_E2M1, 1>(a, pl.cfg, grid2, st);
+        break;
+    }
+    SGLQ_HIP(hipGetLastError());
+    if (pl.nz > 1) {
+      k_splitk_reduce<<<dim3((unsigned)((d->N + 255) / 256), (unsigned)M), 256, 0, st>>>(
+          part, pl.nz, (int)M, (int)d->N, rowexp,
+          d->kind == SGLQ_KIND_E2M1 ? d->colexp : nullptr, bias, C, ldc);
+      SGLQ_HIP(hipGetLastError());
+    }
+    return 0;
+  }
   switch (d->kind) {
     case SGLQ_KIND_U4:
       launch_split<SGLQ_KIND_U4>(a, split, d->scf16, stepm, variant, bn, grid, lds, st);
@@ -598,12 +1033,18 @@ int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
               float *C, int64_t ldc, hipStream_t st) {
   const int split = dt == SGLQ_DT_F32;
   const int64_t bmr = sglq_gemm_rows(d, split);
-  const int64_t Mpad = (M + bmr - 1) / bmr * bmr;
+  const int64_t Mpad = (M + 255) / 256 * 256;  // whole 128- and 256-row blocks
   const size_t aop_bytes = sglq_aop_bytes(d, Mpad, split);
-  if (sglq_ws_reserve(d, aop_bytes + (size_t)Mpad * sizeof(int) + 256) != 0) return -1;
+  const size_t o_part = (aop_bytes + (size_t)Mpad * sizeof(int) + 255) / 256 * 256;
+  const size_t part_bytes =
+      lds_direct(d) ? (size_t)lds_plan(d, M).nz * M * d->N * sizeof(float) : 0;
+  if (sglq_ws_reserve(d, o_part + part_bytes + 256) != 0) return -1;
   void *aop = d->ws;
   int *rowexp = (int *)((char *)d->ws + aop_bytes);
+  float *part = part_bytes > (size_t)M * d->N * sizeof(float) ? (float *)((char *)d->ws + o_part)
+                                                              : nullptr;
   if (sglq_prep_a(d, 0, A, dt, lda, M, Mpad, nullptr, 0, split, aop, rowexp, st) != 0)
     return -1;
-  return sglq_gemm_run(d, nullptr, aop, rowexp, M, Mpad, Mpad / bmr, split, bias, C, ldc, st);
+  return sglq_gemm_run(d, nullptr, aop, rowexp, M, Mpad, Mpad / bmr, split, bias, C, ldc, part,
+                       st);
 }

@@ -212,13 +212,13 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
                       (int *)(ws + o_rexp1), st) != 0)
         return -1;
       if (sglq_gemm_run(g0, &g1, ws + o_aop1, (const int *)(ws + o_rexp1), P, Mpad, maxblk,
-                        split1, nullptr, gu, 2 * mi, st) != 0)
+                        split1, nullptr, gu, 2 * mi, nullptr, st) != 0)
         return -1;
       if (sglq_prep_a(d0, 2, gu, SGLQ_DT_F32, 2 * mi, P, Mpad, nullptr, (int)mi, 1,
                       ws + o_aop2, (int *)(ws + o_rexp2), st) != 0)
         return -1;
       if (sglq_gemm_run(d0, &g2, ws + o_aop2, (const int *)(ws + o_rexp2), P, Mpad, maxblk, 1,
-                        nullptr, o, E, st) != 0)
+                        nullptr, o, E, nullptr, st) != 0)
         return -1;
     }
     dim3 grid((unsigned)((E + 255) / 256), (unsigned)T);

@@ -108,7 +108,7 @@ size_t sglq_aop_bytes(const sglq_dev *d, int64_t Mpad, int split);
 // nblk row blocks (dense: block b = rows [128b, 128b+128); grouped: from grp->segs).
 int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop, const int *rowexp,
                   int64_t M, int64_t Mpad, int64_t nblk, int split, const float *bias, float *C,
-                  int64_t ldc, hipStream_t st);
+                  int64_t ldc, float *part, hipStream_t st);
 // Grouped decode GEMV (MoE): one launch over the row segments of grp (each <= max_rows rows of
 // one expert, at most max_segs of them), activation rows per amode (0 A row r, 1 A row
 // rowmap[r], 2 silu(A[r][k]) * A[r][kcols + k] with f32 A; A has a_rows rows).  Only when every workgroup can take

@@ -76,20 +76,12 @@ def test_marlin_equals_natural(orc):
     assert torch.equal(mar.dequant(), nat.dequant())
 
 
-@pytest.mark.parametrize("shape", [(11008, 4096), (4096, 11008)])
-def test_gptq_llama7b_mlp(orc, shape):
-    """BASELINE config 2 at full size, M = 1 and 16, f32 and bf16 activations."""
-    _run(orc, "gptq4", shape[0], shape[1], [1, 16], seed=0x5EED0002)
-
-
-def test_w8_qwen05_mlp(orc):
-    """BASELINE config 1 at full size: [4864, 896], M = 1 and 8, f32 activations."""
-    _run(orc, "w8", 4864, 896, [1, 8], dtypes=("f32",), seed=0x5EED0001)
-
-
-def test_mxfp4_8192(orc):
-    """BASELINE config 4 at full size, M = 1 and 16, bf16 activations."""
-    _run(orc, "mxfp4", 8192, 8192, [1, 16], dtypes=("bf16",), seed=0x5EED0004)
+@pytest.mark.parametrize("fmt", ["gptq4", "awq4", "mxfp4", "w8", "gptq8"])
+def test_prefill_split_over_k(orc, fmt):
+    """Prefill GEMM tilings at K = 4096 and ragged N: 64 x 128 tiles split 6 ways over K
+    (M <= 64), 128 x 64 tiles split 3 ways (M = 100) and unsplit (M = 200); slice partials are
+    reduced in order."""
+    _run(orc, fmt, 1000, 4096, [33, 64, 100, 200], dtypes=("bf16",), bias=True)
 
 
 def test_graph_replay_matches_eager(orc):
@@ -123,5 +115,6 @@ def test_deterministic_split_k(orc):
     import torch
     kind, a = build("gptq4", 4096, 11008, seed=23)
     ql = product(kind, a, 4096, 11008)
-    A = torch.from_numpy(synth.normal(24, (16, 11008))).cuda()
-    assert torch.equal(ql.forward(A), ql.forward(A))
+    for M in (16, 64, 256):
+        A = torch.from_numpy(synth.normal(24, (M, 11008))).cuda()
+        assert torch.equal(ql.forward(A), ql.forward(A)), M
