@@ -523,14 +523,13 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 }
 
 // Prefill GEMM with the weight tile dequantized once per workgroup into LDS (the "direct"
-// formats: prescaled U4/U8 groups and MXFP4).  128 x BN tile, 4 waves (2 x 2, each 64 x BN/2),
-// pipelined over stages of two MFMA steps: while the MFMAs of stage s read the A operands and
-// the f16 weights of stage s from one LDS buffer, the global loads of stage s + 1 are in flight;
-// their codes are then unpacked (each code once per workgroup, not once per wave) into the other
-// buffer.  LDS per workgroup: 2 x (16 KiB per A piece + BN/16 x 2 KiB), so two workgroups
-// share a CU.
-template <int KIND, int NP, int BN, int SSX, int WMW>
-__global__ __launch_bounds__(128 * WMW) void k_gemm_lds(GemmArgs a) {
+// formats: prescaled U4/U8 groups and MXFP4).  (64 WMW) x BN tile, 2 WMW waves (WMW along M x 2
+// along N, each 64 x BN/2), pipelined over stages of two MFMA steps through a ring of NBUF LDS
+// buffers.  Each stage's A operands are copied and its weight codes unpacked (each code once
+// per workgroup, not once per wave) into a buffer while the MFMAs read another one; blockIdx.y
+// selects a slice of the stages when the call is split over K.
+template <int KIND, int NP, int BN, int SSX, int WMW, int NBUF>
+__global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
   constexpr int SS = SSX < SPC ? SSX : SPC;  // MFMA steps per stage
   constexpr int HPC = SPC / SS;         // stages per chunk
@@ -544,9 +543,9 @@ __global__ __launch_bounds__(128 * WMW) void k_gemm_lds(GemmArgs a) {
   constexpr int AIPT = AITEMS / NTH;
   constexpr int BITEMS = NT16 * SS * 64;     // 16-B weight operands per stage
   constexpr int PB = NT16 * 64 / NTH;        // (tile, lane) code words per thread
-  extern __shared__ half8_t s_lds[];         // [2][AITEMS] A, then [2][BITEMS] B
+  extern __shared__ half8_t s_lds[];         // [NBUF][AITEMS] A, then [NBUF][BITEMS] B
   half8_t *s_a = s_lds;
-  half8_t *s_b = s_lds + 2 * AITEMS;
+  half8_t *s_b = s_lds + NBUF * AITEMS;
 
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int wm = w % WMW, wn = w / WMW;
@@ -590,8 +589,7 @@ __global__ __launch_bounds__(128 * WMW) void k_gemm_lds(GemmArgs a) {
   constexpr int RPI = NTH / BMR;  // 2
   const int64_t plane = (int64_t)a.nsteps * 4 * a.Mpad;
   const half8_t *abase = a.aop + m0 + (tid % BMR) + (int64_t)(tid / BMR) * a.Mpad;
-  half8_t areg[AIPT];
-  auto load_a = [&](int st) {
+  auto load_a = [&](int st, half8_t(&areg)[AIPT]) {
 #pragma unroll
     for (int q = 0; q < AIPT; q++) {
       const int r = RPI * q;  // + tid / BMR (in abase)
@@ -599,7 +597,7 @@ __global__ __launch_bounds__(128 * WMW) void k_gemm_lds(GemmArgs a) {
       areg[q] = ldg(abase + p * plane + ((int64_t)st * SS * 4 + sj) * a.Mpad);
     }
   };
-  auto store_a = [&](int buf) {
+  auto store_a = [&](int buf, const half8_t(&areg)[AIPT]) {
 #pragma unroll
     for (int q = 0; q < AIPT; q++) s_a[buf * AITEMS + tid + NTH * q] = areg[q];
   };
@@ -618,9 +616,7 @@ __global__ __launch_bounds__(128 * WMW) void k_gemm_lds(GemmArgs a) {
                                  ((int64_t)t * 16 + (lb & 15)) * a.nmeta * (E2M1 ? 1 : 4));
     if constexpr (E2M1) cref[q] = colexp[t * 16 + (lb & 15)];
   }
-  u32x4_t breg[PB];
-  MT mreg[PB];
-  auto load_b = [&](int st) {
+  auto load_b = [&](int st, u32x4_t(&breg)[PB], MT(&mreg)[PB]) {
     const int c = st / HPC, h = st % HPC;
     const int g = c / a.cpg;
 #pragma unroll
@@ -640,7 +636,7 @@ __global__ __launch_bounds__(128 * WMW) void k_gemm_lds(GemmArgs a) {
         mreg[q] = ldg(msrc[q] + g);
     }
   };
-  auto store_b = [&](int buf) {
+  auto store_b = [&](int buf, const u32x4_t(&breg)[PB], const MT(&mreg)[PB]) {
 #pragma unroll
     for (int q = 0; q < PB; q++) {
       const int pp = tid + NTH * q, tb = pp >> 6, lb = pp & 63;
@@ -672,41 +668,69 @@ __global__ __launch_bounds__(128 * WMW) void k_gemm_lds(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < TN; j++) acc[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
 
-  load_a(st0);
-  load_b(st0);
-  store_a(0);
-  store_b(0);
-  __syncthreads();
-  for (int st = st0; st < st1; st++) {
-    const int buf = (st - st0) & 1;
-    const bool more = st + 1 < st1;
-    if (more) {
-      load_a(st + 1);
-      load_b(st + 1);
-    }
+  // all operands of one stage are read from LDS before its MFMAs, so the reads overlap each
+  // other and the MFMAs wait once
+  auto compute = [&](int buf) {
     const half8_t *sa = s_a + buf * AITEMS + wm * 64 + n16;
     const half8_t *sb = s_b + buf * BITEMS + wn * TN * SS * 64 + lane;
+    half8_t bv[SS][TN], av[SS][NP][MB];
 #pragma unroll
     for (int s = 0; s < SS; s++) {
-      half8_t bv[TN];
 #pragma unroll
-      for (int j = 0; j < TN; j++) bv[j] = sb[(j * SS + s) * 64];
+      for (int j = 0; j < TN; j++) bv[s][j] = sb[(j * SS + s) * 64];
 #pragma unroll
-      for (int i = 0; i < MB; i++) {
+      for (int p = 0; p < NP; p++)
 #pragma unroll
-        for (int p = 0; p < NP; p++) {
-          const half8_t av = sa[((p * SS + s) * 4 + kq) * BMR + i * 16];
+        for (int i = 0; i < MB; i++) av[s][p][i] = sa[((p * SS + s) * 4 + kq) * BMR + i * 16];
+    }
+#pragma unroll
+    for (int s = 0; s < SS; s++)
+#pragma unroll
+      for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int i = 0; i < MB; i++)
 #pragma unroll
           for (int j = 0; j < TN; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[j], acc[i][j], 0, 0, 0);
-        }
-      }
+            acc[i][j] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(av[s][p][i], bv[s][j], acc[i][j], 0, 0, 0);
+  };
+
+  // One register set and NBUF LDS buffers in a ring.  NBUF = 2: iteration r loads stage r + 1,
+  // multiplies stage r, then writes stage r + 1 into the other buffer.  NBUF = 3: iteration r
+  // writes stage r + 1 (loaded during iteration r - 1) into buffer (r + 1) % 3, loads stage
+  // r + 2 and multiplies stage r, so the loads of a stage have a whole iteration in flight.
+  // One barrier per iteration; the loop body is uniform (past the end it reloads the last
+  // stage into a buffer nobody reads).
+  half8_t ar[AIPT];
+  u32x4_t br[PB];
+  MT mr[PB];
+  load_a(st0, ar);
+  load_b(st0, br, mr);
+  store_a(0, ar);
+  store_b(0, br, mr);
+  if constexpr (NBUF == 3) {
+    load_a(min(st0 + 1, st1 - 1), ar);
+    load_b(min(st0 + 1, st1 - 1), br, mr);
+  }
+  __syncthreads();
+  int bc = 0;  // buffer of stage r
+  for (int st = st0; st < st1; st++) {
+    const int bn1 = bc == NBUF - 1 ? 0 : bc + 1;
+    if constexpr (NBUF == 3) {
+      store_a(bn1, ar);
+      store_b(bn1, br, mr);
     }
-    if (more) {
-      store_a(buf ^ 1);
-      store_b(buf ^ 1);
-      __syncthreads();
+    const int nx = min(st + NBUF - 1, st1 - 1);
+    load_a(nx, ar);
+    load_b(nx, br, mr);
+    __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the MFMAs
+    compute(bc);
+    if constexpr (NBUF == 2) {
+      store_a(bn1, ar);
+      store_b(bn1, br, mr);
     }
+    __syncthreads();
+    bc = bn1;
   }
 
   // epilogue: lane holds rows 4*kq + r of each 16-row block, column n16 of each tile
@@ -761,35 +785,38 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
   C[(int64_t)m * ldc + n] = ldexpf(s, rowexp[m] + ce) + (bias ? bias[n] : 0.f);
 }
 
-template <int KIND, int NP, int BN, int SSX, int WMW>
-void launch_lds1(const GemmArgs &a, dim3 grid, size_t lds, hipStream_t st) {
+template <int KIND, int NP, int BN, int SSX, int WMW, int NBUF>
+void launch_lds1(const GemmArgs &a, dim3 grid, hipStream_t st) {
   static bool raised = false;
-  auto f = k_gemm_lds<KIND, NP, BN, SSX, WMW>;
-  if (!raised)
-    raised = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 160 * 1024) == hipSuccess;
-  f<<<grid, 128 * WMW, lds, st>>>(a);
+  constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
+  constexpr int SS = SSX < SPC ? SSX : SPC;
+  // LDS: NBUF x (A: NP pieces x SS steps x 4 x rows, B: BN/16 tiles x SS steps x 64) x 16 B
+  constexpr size_t lds = (size_t)NBUF * (NP * SS * 4 * 64 * WMW + (BN / 16) * SS * 64) * 16;
+  if constexpr (lds > 160 * 1024) {
+    // too big with two A pieces: the same tile with 2-step stages and two buffers (fits)
+    static_assert(SSX != 2 || NBUF != 2, "k_gemm_lds tile exceeds the LDS");
+    launch_lds1<KIND, NP, BN, 2, WMW, 2>(a, grid, st);
+  } else {
+    auto f = k_gemm_lds<KIND, NP, BN, SSX, WMW, NBUF>;
+    if (!raised)
+      raised = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   160 * 1024) == hipSuccess;
+    f<<<grid, 128 * WMW, lds, st>>>(a);
+  }
 }
 
-// LDS bytes of k_gemm_lds<.., BN, SSX, WMW>
-size_t lds_bytes(int spc, int np, int bn, int ssx, int wmw) {
-  const int ss = ssx < spc ? ssx : spc;
-  return (size_t)2 * (np * ss * 4 * 64 * wmw * 16 + (bn / 16) * ss * 64 * 16);
-}
-
-// tile configurations of k_gemm_lds: rows x columns per workgroup
-enum { LDS_128x128 = 0, LDS_128x64 = 1, LDS_256x128 = 2, LDS_64x128 = 3 };
-int lds_rows(int cfg) { return cfg == LDS_256x128 ? 256 : cfg == LDS_64x128 ? 64 : 128; }
+// tile configurations of k_gemm_lds (rows x columns per workgroup; ring depth 2 or 3); all
+// stages are two MFMA steps
+enum { LDS_64x128 = 0, LDS_128x64 = 1, LDS_256x128 = 2 };
+int lds_rows(int cfg) { return cfg == LDS_256x128 ? 256 : cfg == LDS_128x64 ? 128 : 64; }
 int lds_cols(int cfg) { return cfg == LDS_128x64 ? 64 : 128; }
 
 template <int KIND, int NP>
 void launch_lds(const GemmArgs &a, int cfg, dim3 grid, hipStream_t st) {
-  const int spc = KIND == SGLQ_KIND_U8 ? 2 : 4;
   switch (cfg) {
-    case LDS_128x64: launch_lds1<KIND, NP, 64, 2, 2>(a, grid, lds_bytes(spc, NP, 64, 2, 2), st); break;
-    case LDS_256x128: launch_lds1<KIND, NP, 128, 2, 4>(a, grid, lds_bytes(spc, NP, 128, 2, 4), st); break;
-    case LDS_64x128: launch_lds1<KIND, NP, 128, 2, 1>(a, grid, lds_bytes(spc, NP, 128, 2, 1), st); break;
-    default: launch_lds1<KIND, NP, 128, 2, 2>(a, grid, lds_bytes(spc, NP, 128, 2, 2), st); break;
+    case LDS_64x128: launch_lds1<KIND, NP, 128, 2, 1, 2>(a, grid, st); break;
+    case LDS_256x128: launch_lds1<KIND, NP, 128, 2, 4, 3>(a, grid, st); break;
+    default: launch_lds1<KIND, NP, 64, 2, 2, 2>(a, grid, st); break;
   }
 }
 
@@ -970,7 +997,7 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
   const int stepm = d->meta_mode == SGLQ_META_STEP;
   // direct formats with f16-exact scales: the LDS-dequant kernel
   if (lds_direct(d)) {
-    const LdsPlan pl = grp ? LdsPlan{bn == 64 ? LDS_128x64 : LDS_128x128, 1} : lds_plan(d, M);
+    const LdsPlan pl = grp ? LdsPlan{LDS_128x64, 1} : lds_plan(d, M);
     if (pl.nz > 1 && !part) {
       sglq_log_error("prefill GEMM: no workspace for the split over K");
       return -1;
