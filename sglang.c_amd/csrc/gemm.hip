@@ -58,6 +58,12 @@ __device__ __forceinline__ float prep_value(const void *A, int dt, int64_t rb, i
   }
 }
 
+// exponent e with |a| / 2^e in [2^13, 2^14) for the row's largest finite |a| = mx (0 for rows
+// of zeros, infinities or NaNs only)
+__device__ __forceinline__ int row_exponent(float mx) {
+  return (mx > 0.f && mx <= 3.0e38f) ? ilogbf(mx) - 13 : 0;
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256) void k_rowexp(const void *__restrict__ A, int dt, int64_t lda,
                                                 int M, int Mpad, int K, int nsteps,
@@ -111,7 +117,7 @@ __global__ __launch_bounds__(256) void k_rowexp(const void *__restrict__ A, int 
     }
   }
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  if (lane == 0) rowexp[m] = (mx > 0.f && mx <= 3.0e38f) ? ilogbf(mx) - 13 : 0;
+  if (lane == 0) rowexp[m] = row_exponent(mx);
 }
 
 template <int MODE>
@@ -121,7 +127,8 @@ __global__ __launch_bounds__(256) void k_prep_a(const void *__restrict__ A, int 
                                                 const int32_t *__restrict__ rowmap, int kcols,
                                                 int perm4, int split, int vec,
                                                 half8_t *__restrict__ aop,
-                                                const int *__restrict__ rowexp) {
+                                                const int *__restrict__ rowmax,
+                                                int *__restrict__ rowexp) {
   const int nitems = nsteps * 4;  // it = step * 4 + kq
   const int64_t plane = (int64_t)nitems * Mpad;  // 16-B items per piece
 #pragma unroll
@@ -131,7 +138,13 @@ __global__ __launch_bounds__(256) void k_prep_a(const void *__restrict__ A, int 
     const int m = blockIdx.x * 16 + r;
     if (it >= nitems) continue;
     const int64_t src = prep_src<MODE>(rowmap, M, m);
-    const int e = rowexp[m];
+    int e;
+    if (rowmax) {  // row maxima from the producing kernel: the exponent is derived here
+      e = row_exponent(__int_as_float(rowmax[m]));
+      if (it == 0) rowexp[m] = e;
+    } else {
+      e = rowexp[m];
+    }
     float v[8];
     if (src < 0) {
 #pragma unroll
@@ -198,6 +211,8 @@ struct GemmArgs {
   int M, Mpad, N, ntile, nchunk, nsteps, nmeta, cpg, nbn;
   int nbm, xmap;  // dense: row blocks; 1 = XCD-aware tile order (see k_gemm)
   float *part;    // k_gemm_lds split over K: unscaled partial sums [gridDim.y][M][N], else null
+  int swiglu;     // k_gemm_lds grouped: mi > 0 = C gets silu(gate) * up, [rows][mi] (see there)
+  int *rowmax;    // with swiglu: per row, bits of the largest |C| (atomic max, preset to 0)
 };
 
 union H8 {
@@ -610,7 +625,13 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
 #pragma unroll
   for (int q = 0; q < PB; q++) {
     const int pp = tid + NTH * q, tb = pp >> 6, lb = pp & 63;
-    const int t = min(bn * NT16 + tb, a.ntile - 1);
+    int t;
+    if (a.swiglu) {  // a wave's tiles alternate gate tile g, up tile g + mi / 16
+      const int jj = tb % TN, mt = a.swiglu / 16;
+      t = min(bn * (NT16 / 2) + (tb / TN) * (TN / 2) + jj / 2, mt - 1) + (jj & 1) * mt;
+    } else {
+      t = min(bn * NT16 + tb, a.ntile - 1);
+    }
     bsrc[q] = codes + (int64_t)t * a.nchunk * 64 + lb;
     msrc[q] = (const uint32_t *)((const char *)meta +
                                  ((int64_t)t * 16 + (lb & 15)) * a.nmeta * (E2M1 ? 1 : 4));
@@ -734,6 +755,49 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
   }
 
   // epilogue: lane holds rows 4*kq + r of each 16-row block, column n16 of each tile
+  if (a.swiglu) {
+    // MoE gate/up: C[m][n] = silu(g) * u with g, u the gate and up outputs (g / (1 + expf(-g))
+    // as reference src/deepseek.c:662-663), and the row maxima of |C| for the next prep
+    const int tg = bn * (NT16 / 2) + wn * (TN / 2), mi = a.swiglu;
+    float rmx[MB][4];
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) rmx[i][r] = 0.f;
+#pragma unroll
+    for (int pj = 0; pj < TN / 2; pj++) {
+      const int n = (tg + pj) * 16 + n16;
+      if (n >= mi) continue;
+      const int ceg = E2M1 ? (int)colexp[n] - 127 : 0;
+      const int ceu = E2M1 ? (int)colexp[n + mi] - 127 : 0;
+#pragma unroll
+      for (int i = 0; i < MB; i++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int m = m0 + wm * 64 + i * 16 + 4 * kq + r;
+          if (m < mend) {
+            const float g = ldexpf(acc[i][2 * pj][r], a.rowexp[m] + ceg);
+            const float u = ldexpf(acc[i][2 * pj + 1][r], a.rowexp[m] + ceu);
+            const float v = (g / (1.0f + expf(-g))) * u;
+            a.C[(int64_t)m * a.ldc + n] = v;
+            rmx[i][r] = fmaxf(rmx[i][r], fabsf(v));
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < MB; i++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        float x = rmx[i][r];
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));  // the row's 16 lanes
+        const int m = m0 + wm * 64 + i * 16 + 4 * kq + r;
+        if (n16 == 0 && m < mend) atomicMax(&a.rowmax[m], __float_as_int(x));
+      }
+    }
+    return;
+  }
   const int t0 = bn * NT16 + wn * TN;
   if (a.part) {  // split over K: raw partial sums, scaled by k_splitk_reduce
     float *pp = a.part + (int64_t)blockIdx.y * a.M * a.N;
@@ -880,19 +944,20 @@ void launch_split(const GemmArgs &a, bool split, int scf16, int stepm, int varia
 
 int sglq_prep_a(const sglq_dev *d, int mode, const void *A, int dt, int64_t lda, int64_t M,
                 int64_t Mpad, const int32_t *rowmap, int kcols, int split, void *aop,
-                int *rowexp, hipStream_t st) {
+                int *rowexp, hipStream_t st, const int *rowmax) {
   const int32_t *kmap = d->kident ? nullptr : d->kmap;
   const int perm4 = d->kind == SGLQ_KIND_U4;
   const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
   const int vec = kmap == nullptr && (uintptr_t)A % 16 == 0 && (lda * esz) % 16 == 0;
   const dim3 pgrid((unsigned)(Mpad / 16), (unsigned)((d->nsteps * 4 + 63) / 64));
-#define SGLQ_PREP(MODE)                                                                         \
-  k_rowexp<MODE><<<(unsigned)((Mpad + 3) / 4), 256, 0, st>>>(A, dt, lda, (int)M, (int)Mpad,       \
-                                                             (int)d->K, (int)d->nsteps, kmap,     \
-                                                             rowmap, kcols, vec, rowexp);              \
+#define SGLQ_PREP(MODE)                                                                       \
+  if (!rowmax)                                                                                  \
+    k_rowexp<MODE><<<(unsigned)((Mpad + 3) / 4), 256, 0, st>>>(                                 \
+        A, dt, lda, (int)M, (int)Mpad, (int)d->K, (int)d->nsteps, kmap, rowmap, kcols, vec,     \
+        rowexp);                                                                                \
   k_prep_a<MODE><<<pgrid, 256, 0, st>>>(A, dt, lda, (int)M, (int)Mpad, (int)d->K, (int)d->nsteps, \
                                         kmap, rowmap, kcols, perm4, split, vec, (half8_t *)aop,   \
-                                        rowexp)
+                                        rowmax, rowexp)
   if (mode == 0) {
     SGLQ_PREP(0);
   } else if (mode == 1) {
@@ -920,6 +985,8 @@ static bool lds_direct(const sglq_dev *d) {
                       (d->prescale && d->meta_mode == SGLQ_META_GROUP);
   return direct && (d->kind == SGLQ_KIND_E2M1 || d->scf16);
 }
+
+bool sglq_gemm_lds_direct(const sglq_dev *d) { return lds_direct(d); }
 
 // k_gemm_lds tiling of a dense call: 64 x 128 tiles for M <= 64, 128 x 64 below M = 1024, then
 // 256 x 128; and a split over K (deterministic, reduced in slice order) when the tiles alone
@@ -971,6 +1038,8 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
     a.colexp_e = grp->colexp;
     a.segs = (const int4 *)grp->segs;
     a.nseg = grp->nseg;
+    a.swiglu = grp->swiglu;
+    a.rowmax = grp->rowmax;
   }
   a.aop = (const half8_t *)aop;
   a.rowexp = rowexp;
@@ -995,17 +1064,22 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
   }
 
   const int stepm = d->meta_mode == SGLQ_META_STEP;
+  if (grp && grp->swiglu && (!lds_direct(d) || grp->swiglu % 16 != 0)) {
+    sglq_log_error("grouped GEMM: the fused SwiGLU needs the LDS kernel and mi %% 16 == 0");
+    return -1;
+  }
   // direct formats with f16-exact scales: the LDS-dequant kernel
   if (lds_direct(d)) {
-    const LdsPlan pl = grp ? LdsPlan{LDS_128x64, 1} : lds_plan(d, M);
+    const LdsPlan pl = grp ? LdsPlan{LDS_64x128, 1} : lds_plan(d, M);
     if (pl.nz > 1 && !part) {
       sglq_log_error("prefill GEMM: no workspace for the split over K");
       return -1;
     }
     const int cbm = lds_rows(pl.cfg), cbn = lds_cols(pl.cfg);
-    // grouped: row blocks of one expert each (at most 128 rows); dense: the rows of M
+    // grouped: row blocks of one expert each (at most 64 rows); dense: the rows of M
     const int64_t nbm2 = grp ? nblk : (M + cbm - 1) / cbm;
     a.nbn = (int)((d->N + cbn - 1) / cbn);
+    if (a.swiglu) a.nbn = (int)((a.swiglu / 16 + cbn / 32 - 1) / (cbn / 32));  // gate tiles / 2
     a.nbm = (int)nbm2;
     a.xmap = 0;
     a.part = pl.nz > 1 ? part : nullptr;

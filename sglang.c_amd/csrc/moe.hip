@@ -3,13 +3,15 @@
 // branch :660-664; routing itself is an input).
 //
 // Launches, all on the caller's stream, no host synchronisation:
-//   k_moe_route   one workgroup: counts (token, slot) pairs per expert, orders them by expert
-//                 (inside an expert by pair index, so the order is deterministic), and writes
-//                 the row-block table of the grouped GEMMs (blocks of <= 128 rows of one expert)
+//   k_moe_route   one workgroup: counts (token, slot) pairs per expert, gives each pair a row
+//                 among its expert's rows (experts in index order), and writes
+//                 the row-block table of the grouped GEMMs (blocks of <= 64 rows of one expert)
 //   prefill:  prep (gather) A operands of the expert-sorted rows of h
 //             grouped GEMM  gu = h_rows * Wgu[e]^T, each row block with its expert's weights
 //             prep (SwiGLU) A operands of silu(gu[:, :mi]) * gu[:, mi:]
 //             grouped GEMM  o = a * Wdn[e]^T
+//             (weights that take the LDS-dequant GEMM: the gate/up GEMM writes silu(g) * u
+//             and its row maxima itself, and the down prep only converts)
 //   decode (T <= 4): the same two products as grouped decode GEMVs that gather the token rows
 //             and form the SwiGLU rows while staging their activations
 //   k_moe_combine out[t] = sum_j w[t,j] * o[row of (t,j)], slots added in order j = 0..k-1
@@ -21,68 +23,75 @@ namespace {
 
 constexpr int kMaxExperts = 256;
 
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u = __shfl_up(v, d, 64);
+    if (lane >= d) v += u;
+  }
+  return v;
+}
+
+// One workgroup.  Each pair p = t * k + j with a valid expert gets a row among that expert's
+// rows (experts in index order); rowmap[row] = token, pos[p] = row.  Which of its expert's rows
+// a pair gets depends on the order of the LDS atomics, but no result does: each row's product
+// depends only on its token and its expert, and the combine reads rows through pos in slot
+// order.  Row blocks hold at most bm rows of one expert: segs[b] = {expert, first row, rows, 0}.
 __global__ __launch_bounds__(1024) void k_moe_route(const int32_t *__restrict__ ids, int P,
-                                                    int k, int n_exp, int32_t *__restrict__ rowmap,
+                                                    int k, int n_exp, int bm,
+                                                    int32_t *__restrict__ rowmap,
                                                     int32_t *__restrict__ pos,
                                                     int *__restrict__ segs,
-                                                    int *__restrict__ nseg) {
-  __shared__ int run[kMaxExperts];       // next free row of each expert
-  __shared__ int wc[16][kMaxExperts];    // per-wave counts of the current block of pairs
+                                                    int *__restrict__ nseg,
+                                                    int *__restrict__ rowmax) {
+  __shared__ int run[kMaxExperts];  // rows of each expert, then its next free row
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  for (int e = tid; e < n_exp; e += 1024) run[e] = 0;
-  for (int r = tid; r < P; r += 1024) rowmap[r] = -1;  // rows past the routed pairs: zero rows
+  for (int e = tid; e < kMaxExperts; e += 1024) run[e] = 0;
+  for (int r = tid; r < P; r += 1024) {
+    rowmap[r] = -1;  // rows past the routed pairs: zero rows
+    if (rowmax) rowmax[r] = 0;  // for the fused SwiGLU's row maxima
+  }
   __syncthreads();
   for (int p = tid; p < P; p += 1024) {
     const int e = ids[p];
     if (e >= 0 && e < n_exp) atomicAdd(&run[e], 1);
   }
   __syncthreads();
-  if (tid == 0) {  // exclusive scan + row-block table
-    int off = 0, nb = 0;
-    for (int e = 0; e < n_exp; e++) {
-      const int c = run[e];
-      for (int r = 0; r < c; r += SGLQ_GEMM_BM) {
+  if (w == 0) {  // exclusive scans of rows and of row blocks over the experts, 4 per lane
+    int c[4], rs = 0, bs = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      c[q] = run[lane * 4 + q];
+      rs += c[q];
+      bs += (c[q] + bm - 1) / bm;
+    }
+    const int ri = wave_incl_scan(rs, lane), bi = wave_incl_scan(bs, lane);
+    int off = ri - rs, nb = bi - bs;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int e = lane * 4 + q;
+      for (int r = 0; r < c[q]; r += bm) {
         segs[nb * 4 + 0] = e;
         segs[nb * 4 + 1] = off + r;
-        segs[nb * 4 + 2] = min(SGLQ_GEMM_BM, c - r);
+        segs[nb * 4 + 2] = min(bm, c[q] - r);
         segs[nb * 4 + 3] = 0;
         nb++;
       }
       run[e] = off;
-      off += c;
+      off += c[q];
     }
-    *nseg = nb;
+    if (lane == 63) *nseg = bi;
   }
   __syncthreads();
-  const uint64_t lt = (1ull << lane) - 1ull;
-  for (int b = 0; b < P; b += 1024) {
-    const int p = b + tid;
-    const int e = p < P ? ids[p] : -1;
-    const bool ok = e >= 0 && e < n_exp;
-    int rank = 0;
-    for (int ee = 0; ee < n_exp; ee++) {
-      const uint64_t m = __ballot(ok && e == ee);
-      if (ok && e == ee) rank = __popcll(m & lt);
-      if (lane == 0) wc[w][ee] = __popcll(m);
+  for (int p = tid; p < P; p += 1024) {
+    const int e = ids[p];
+    if (e >= 0 && e < n_exp) {
+      const int dst = atomicAdd(&run[e], 1);
+      rowmap[dst] = p / k;
+      pos[p] = dst;
+    } else {
+      pos[p] = -1;
     }
-    __syncthreads();
-    if (p < P) {
-      if (ok) {
-        int dst = run[e] + rank;
-        for (int ww = 0; ww < w; ww++) dst += wc[ww][e];
-        rowmap[dst] = p / k;
-        pos[p] = dst;
-      } else {
-        pos[p] = -1;
-      }
-    }
-    __syncthreads();
-    for (int ee = tid; ee < n_exp; ee += 1024) {
-      int s = 0;
-      for (int ww = 0; ww < 16; ww++) s += wc[ww][ee];
-      run[ee] += s;
-    }
-    __syncthreads();
   }
 }
 
@@ -140,7 +149,7 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
   if (T == 0) return 0;
   {
     const int64_t E = g0->K, mi = d0->K, P = T * k;
-    const int64_t maxblk = (P + SGLQ_GEMM_BM - 1) / SGLQ_GEMM_BM + n_exp;
+    const int64_t maxblk = (P + SGLQ_MOE_BM - 1) / SGLQ_MOE_BM + n_exp;
     const int64_t Mpad = (P + SGLQ_GEMM_BM - 1) / SGLQ_GEMM_BM * SGLQ_GEMM_BM + SGLQ_GEMM_BM;
     const int split1 = h_dtype == SGLQ_DT_F32;
     // workspace (kept in expert 0's gate_up handle)
@@ -155,6 +164,7 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
     const size_t o_gu = off; off = align256(off + (size_t)Mpad * 2 * mi * 4);
     const size_t o_aop2 = off; off = align256(off + sglq_aop_bytes(d0, Mpad, 1));
     const size_t o_rexp2 = off; off = align256(off + (size_t)Mpad * 4);
+    const size_t o_rmax = off; off = align256(off + (size_t)Mpad * 4);
     const size_t o_o = off; off = align256(off + (size_t)Mpad * E * 4);
     if (sglq_ws_reserve(g0, off) != 0) return -1;
     char *ws = (char *)g0->ws;
@@ -191,20 +201,43 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
     int *nseg = (int *)(ws + o_nseg);
     float *gu = (float *)(ws + o_gu);
     float *o = (float *)(ws + o_o);
-    k_moe_route<<<1, 1024, 0, st>>>(topk_ids, (int)P, k, n_exp, rowmap, pos, segs, nseg);
+    // prefill of LDS-kernel experts: SwiGLU fused into the gate/up GEMM's epilogue
+    const bool decode =
+        T <= 4 && sglq_gemv_grouped_fits(g0, T, split1) && sglq_gemv_grouped_fits(d0, T, 1);
+    const bool fuse = !decode && sglq_gemm_lds_direct(g0) && mi % 16 == 0;
+    int *rowmax = fuse ? (int *)(ws + o_rmax) : nullptr;
+    k_moe_route<<<1, 1024, 0, st>>>(topk_ids, (int)P, k, n_exp, SGLQ_MOE_BM, rowmap, pos, segs,
+                                    nseg, rowmax);
     SGLQ_HIP(hipGetLastError());
     sglq_group g1 = {dp, dp + n_exp, (const uint8_t *const *)(dp + 2 * n_exp), segs, nseg};
     sglq_group g2 = {dp + 3 * n_exp, dp + 4 * n_exp, (const uint8_t *const *)(dp + 5 * n_exp),
                      segs, nseg};
     // decode-sized batches (every expert has at most T <= 4 rows): grouped GEMVs that read the
     // token rows and the SwiGLU rows directly; otherwise operand prep + grouped GEMMs
-    if (T <= 4 && sglq_gemv_grouped_fits(g0, T, split1) && sglq_gemv_grouped_fits(d0, T, 1)) {
+    if (decode) {
       const int64_t max_segs = P < n_exp ? P : n_exp;
       if (sglq_gemv_grouped(g0, &g1, T, max_segs, h, h_dtype, T, E, 1, rowmap, 0, gu, 2 * mi,
                             st) != 0)
         return -1;
       if (sglq_gemv_grouped(d0, &g2, T, max_segs, gu, SGLQ_DT_F32, P, 2 * mi, 2, nullptr,
                             (int)mi, o, E, st) != 0)
+        return -1;
+    } else if (fuse) {
+      // act[r] = silu(gate) * up of row r, [P, mi] f32, written by the gate/up GEMM together
+      // with its row maxima; the down prep derives the row exponents from those
+      g1.swiglu = (int)mi;
+      g1.rowmax = rowmax;
+      if (sglq_prep_a(g0, 1, h, h_dtype, E, P, Mpad, rowmap, 0, split1, ws + o_aop1,
+                      (int *)(ws + o_rexp1), st) != 0)
+        return -1;
+      if (sglq_gemm_run(g0, &g1, ws + o_aop1, (const int *)(ws + o_rexp1), P, Mpad, maxblk,
+                        split1, nullptr, gu, mi, nullptr, st) != 0)
+        return -1;
+      if (sglq_prep_a(d0, 0, gu, SGLQ_DT_F32, mi, P, Mpad, nullptr, 0, 1, ws + o_aop2,
+                      (int *)(ws + o_rexp2), st, rowmax) != 0)
+        return -1;
+      if (sglq_gemm_run(d0, &g2, ws + o_aop2, (const int *)(ws + o_rexp2), P, Mpad, maxblk, 1,
+                        nullptr, o, E, nullptr, st) != 0)
         return -1;
     } else {
       // rows of Mpad beyond P: rowmap entries are never read (prep zeroes rows >= M)

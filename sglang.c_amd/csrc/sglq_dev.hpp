@@ -92,18 +92,25 @@ int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
 
 // Grouped-GEMM building blocks (gemm.hip), used by the MoE path.
 constexpr int SGLQ_GEMM_BM = 128;  // rows per GEMM row block
+constexpr int SGLQ_MOE_BM = 64;    // rows per MoE row block (all of one expert)
 struct sglq_group {               // per-expert weights (device arrays) + device row-block table
   const void *const *codes;       // [n_exp] u32x4_t*
   const void *const *meta;        // [n_exp]
   const uint8_t *const *colexp;   // [n_exp] (MXFP4)
   const int *segs;                // [max blocks][4] {expert, first row, rows, 0}
   const int *nseg;                // blocks in use (device scalar)
+  int swiglu;                     // gate/up weights [2 mi, K]: mi > 0 = C gets silu(g) * u
+  int *rowmax;                    // with swiglu: per-row max |C| bits (atomic max, preset 0)
 };
 // A operands of Mpad rows into aop (sglq_aop_bytes) + row exponents; mode 0 dense rows,
 // 1 rows gathered through rowmap (-1 = zero row), 2 silu(A[m][k]) * A[m][kcols + k] (f32 A).
+// rowmax (optional): per-row max |a| bits already known (the row exponents are derived from
+// them and written to rowexp instead of a pass over the rows).
 int sglq_prep_a(const sglq_dev *d, int mode, const void *A, int dt, int64_t lda, int64_t M,
                 int64_t Mpad, const int32_t *rowmap, int kcols, int split, void *aop,
-                int *rowexp, hipStream_t st);
+                int *rowexp, hipStream_t st, const int *rowmax = nullptr);
+// the prefill GEMM of this weight runs the LDS-dequant kernel (needed for a fused SwiGLU)
+bool sglq_gemm_lds_direct(const sglq_dev *d);
 size_t sglq_aop_bytes(const sglq_dev *d, int64_t Mpad, int split);
 // nblk row blocks (dense: block b = rows [128b, 128b+128); grouped: from grp->segs).
 int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop, const int *rowexp,

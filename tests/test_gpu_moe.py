@@ -12,25 +12,33 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-3
 
 
-def _experts(orc, n_exp, E, mi, seed):
+def _experts(orc, n_exp, E, mi, seed, fmt="gptq4", std=0.02):
     import sgl_qlinear as q
+    from linear_cases import build, oracle_weight, product
     cfg = dict(method=2, bits=4, group_size=128, zero_point=1)
     gu, dn, wgu, wdn = [], [], [], []
     for e in range(n_exp):
         for (N, K, lst, wl, sd) in ((2 * mi, E, gu, wgu, seed + 2 * e),
                                     (E, mi, dn, wdn, seed + 2 * e + 1)):
-            qw, qz, s = synth.gptq_expert(sd, N, K)
-            lst.append(q.QLinear.from_awq_gptq(q.make_cfg(**cfg), qw, s, N, K, qzeros=qz))
-            rc, W = orc.dequant(ocfg(**cfg), qw, s, N, K, qzeros=qz)
-            assert rc == 0
+            if fmt == "gptq4":
+                c, z, s = synth.quantize_groups(synth.normal(sd, (N, K), std), 128)
+                qw, qz = synth.gptq_pack(c, z)
+                lst.append(q.QLinear.from_awq_gptq(q.make_cfg(**cfg), qw, s, N, K, qzeros=qz))
+                rc, W = orc.dequant(ocfg(**cfg), qw, s, N, K, qzeros=qz)
+                assert rc == 0
+            else:
+                kind, a = build(fmt, N, K, seed=sd)
+                lst.append(product(kind, a, N, K))
+                W = oracle_weight(orc, kind, a, N, K)
             wl.append(W)
     return gu, dn, wgu, wdn
 
 
-def _check(orc, n_exp, E, mi, T, k, seed, dtypes=("bf16", "f32"), drop=False):
+def _check(orc, n_exp, E, mi, T, k, seed, dtypes=("bf16", "f32"), drop=False, fmt="gptq4",
+           std=0.02):
     import torch
     import sgl_qlinear as q
-    gu, dn, wgu, wdn = _experts(orc, n_exp, E, mi, seed)
+    gu, dn, wgu, wdn = _experts(orc, n_exp, E, mi, seed, fmt, std)
     ids, wts = synth.moe_routing(seed + 999, T, n_exp, k)
     if drop:  # unrouted slots (id -1) are skipped
         ids[::3, -1] = -1
@@ -41,7 +49,7 @@ def _check(orc, n_exp, E, mi, T, k, seed, dtypes=("bf16", "f32"), drop=False):
             th = torch.from_numpy(hb).cuda().to(torch.bfloat16)
         else:
             hb, th = h, torch.from_numpy(h).cuda()
-        print(f"[gpu] moe n_exp={n_exp} E={E} mi={mi} T={T} k={k} {dt}", flush=True)
+        print(f"[gpu] moe {fmt} n_exp={n_exp} E={E} mi={mi} T={T} k={k} {dt}", flush=True)
         y = q.qmoe_forward(gu, dn, th, torch.from_numpy(ids).cuda(),
                            torch.from_numpy(wts).cuda()).cpu().numpy()
         ref = orc.moe_ffn(hb, wgu, wdn, ids, wts)
@@ -58,6 +66,17 @@ def test_moe_small(orc):
 
 def test_moe_unrouted_slots(orc):
     _check(orc, 6, 256, 256, 9, 3, seed=41, dtypes=("f32",), drop=True)
+
+
+def test_moe_prefill_mxfp4(orc):
+    """MXFP4 experts: the fused SwiGLU epilogue applies the gate and up column exponents."""
+    _check(orc, 8, 256, 128, 40, 2, seed=61, fmt="mxfp4")
+
+
+def test_moe_prefill_unfused(orc):
+    """Group scales below 2^-14 cannot prescale f16 codes: those experts take the register
+    unpack GEMM, with SwiGLU formed by its own operand prep."""
+    _check(orc, 8, 256, 128, 40, 2, seed=71, std=2e-5)
 
 
 def test_moe_decode_batch_f32(orc):
