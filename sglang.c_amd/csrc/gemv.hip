@@ -432,6 +432,25 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  // partials of (row r, column nn) added in K order; eight loads are in flight at a time
+  // (one at a time, each waiting for its predecessor, they made the reduction latency-bound)
+  auto sum_parts = [&](int r, int nn) -> float {
+    const float *pp = a.part + (int64_t)r * a.N + nn;
+    const int64_t ss = (int64_t)M * a.N;
+    float sum = 0.f;
+    int s0 = 0;
+    for (; s0 + 8 <= a.S; s0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++)
+        v[q] = __hip_atomic_load(pp + (s0 + q) * ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int q = 0; q < 8; q++) sum += v[q];
+    }
+    for (; s0 < a.S; s0++)
+      sum += __hip_atomic_load(pp + s0 * ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return sum;
+  };
   if (a.ks > 1) {
     // the ks != 0 waves have left, so no workgroup barrier is possible: arrivals are counted
     // per tile, by its ks == 0 wave
@@ -444,13 +463,8 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
     if (!last) return;
     for (int idx = lane; idx < M * 16; idx += 64) {
       const int r = idx >> 4, nn = t * 16 + (idx & 15);
-      if (tvalid && nn < a.N) {
-        float sum = 0.f;
-        for (int s = 0; s < a.S; s++)
-          sum += __hip_atomic_load(&a.part[((int64_t)s * M + r) * a.N + nn], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        a.C[r * a.ldc + nn] = sum + (a.bias ? a.bias[nn] : 0.f);
-      }
+      if (tvalid && nn < a.N)
+        a.C[r * a.ldc + nn] = sum_parts(r, nn) + (a.bias ? a.bias[nn] : 0.f);
     }
     if (lane == 0) __hip_atomic_store(&a.cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
@@ -464,13 +478,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   const int ncol = a.tpg * 16;
   for (int idx = tid; idx < M * ncol; idx += nthr) {
     const int r = idx / ncol, nn = cg * ncol + idx % ncol;
-    if (nn < a.N) {
-      float sum = 0.f;
-      for (int s = 0; s < a.S; s++)
-        sum += __hip_atomic_load(&a.part[((int64_t)s * M + r) * a.N + nn], __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-      a.C[r * a.ldc + nn] = sum + (a.bias ? a.bias[nn] : 0.f);
-    }
+    if (nn < a.N) a.C[r * a.ldc + nn] = sum_parts(r, nn) + (a.bias ? a.bias[nn] : 0.f);
   }
   if (tid == 0) __hip_atomic_store(&a.cnt[cg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
