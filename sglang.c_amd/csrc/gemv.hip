@@ -540,7 +540,7 @@ struct Plan {
 // Work split for one launch.  A workgroup stages one K range of the activations in LDS and
 // its ks x tpg waves split that range (ks slices of cpw chunks) over tpg tiles; ranges beyond
 // one workgroup (K longer than the staging budget allows) are added across workgroups.
-Plan plan_gemv(const sglq_dev *d, int64_t M, bool split) {
+Plan plan_gemv(const sglq_dev *d, int64_t M, bool split, bool grouped = false) {
   const int64_t np = split ? 2 : 1;
   const int64_t max_chunks = ((int64_t)kLdsBudget / (np * M * 16) - 1) / (d->spc * 4);
   Plan best = {0, 0, 0, 1 << 30, 0, 0};
@@ -556,6 +556,19 @@ Plan plan_gemv(const sglq_dev *d, int64_t M, bool split) {
   }
   if (best.cpw == 0) best = {4, 1, 0, (int)((d->nchunk + 3) / 4), 0, 0};
   best.tpg = best.ks >= 4 ? 1 : 4 / best.ks;
+  // Several rows over a long K: measured fastest with one K slice per wave, four tiles per
+  // workgroup and the K range cut so that about 8-12 workgroups share a column group (many
+  // short workgroups, each staging a short activation range, beat few long ones even with
+  // the partial-sum pass).  One row, or short K, keeps the fewest splits above, and so does
+  // the grouped launch (it needs a single K range).
+  if (!grouped && M >= 2 && d->nchunk >= 24) {
+    for (int cpw : {4, 8, 12}) {
+      const int S = (int)((d->nchunk + cpw - 1) / cpw);
+      if (cpw > max_chunks) break;
+      best = {cpw, 1, 4, S, 0, 0};
+      if (S <= 12) break;
+    }
+  }
   best.ncg = (int)((d->ntile + best.tpg - 1) / best.tpg);
   const size_t stage = (size_t)np * M * (best.ks * best.cpw * d->spc * 4 + 1) * 16;
   const size_t red = (size_t)best.ks * best.tpg * 64 * 16;
@@ -651,7 +664,7 @@ int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
 }
 
 int sglq_gemv_grouped_fits(const sglq_dev *d, int64_t max_rows, int split) {
-  return max_rows <= 16 && plan_gemv(d, max_rows, split).S == 1;
+  return max_rows <= 16 && plan_gemv(d, max_rows, split, true).S == 1;
 }
 
 int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows,
@@ -659,7 +672,7 @@ int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows
                       int amode, const int32_t *rowmap, int kcols, float *C, int64_t ldc,
                       hipStream_t st) {
   const bool split = dt == SGLQ_DT_F32;
-  const Plan pl = plan_gemv(d, max_rows, split);
+  const Plan pl = plan_gemv(d, max_rows, split, true);
   const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
   if (pl.S != 1 || max_rows > 16) {
     sglq_log_error("qlinear: grouped GEMV needs one K range per workgroup (rows %lld)",
