@@ -160,32 +160,50 @@ def gemm_line(torch, ql, M, K, N, dtype, warmup, tag, out):
                 "us": round(t * 1e6, 1)}
 
 
-def extra_configs(torch, q, warmup):
-    """Secondary BASELINE configs, each timed briefly (graph replays)."""
+EXTRA_SECTIONS = ("gemv16", "w8", "mxfp4", "gemm", "moe")
+
+
+def extra_configs(torch, q, warmup, only=EXTRA_SECTIONS):
+    """Secondary BASELINE configs, each timed briefly (graph replays); `only` picks sections."""
     import numpy as np
     import synth
     out = {}
     # config 2 at M = 16 (f32 and bf16), both shapes
     for (N, K, seed) in ((11008, 4096, 0x5EED0002), (4096, 11008, 0x5EED0003)):
+        if "gemv16" not in only:
+            break
         w = gptq_weight(N, K, seed)
         for dt, dn in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
             gemv_line(torch, q, lambda c: make_gptq(q, w, N, K, c), effective_bytes(N, K), [16],
                       dt, warmup, f"gptq_gemv_{N}x{K}_{dn}", out)
     # config 1: W8 per-channel [4864, 896], M = 1 and 8, f32
-    W = synth.normal(0x5EED0001, (4864, 896), 0.02)
-    q8, s8 = synth.quant_rows_i8(W)
-    gemv_line(torch, q, lambda c: [q.QLinear.from_w8(q8, s8) for _ in range(c)],
-              4864 * 896 + 4864 * 4, [1, 8], torch.float32, warmup, "w8_4864x896_f32", out)
+    if "w8" in only:
+        W = synth.normal(0x5EED0001, (4864, 896), 0.02)
+        q8, s8 = synth.quant_rows_i8(W)
+        gemv_line(torch, q, lambda c: [q.QLinear.from_w8(q8, s8) for _ in range(c)],
+                  4864 * 896 + 4864 * 4, [1, 8], torch.float32, warmup, "w8_4864x896_f32", out)
     # config 4: MXFP4 [8192, 8192], M = 1 and 16 (GEMV), 512 (GEMM), bf16
-    Wm = synth.normal(0x5EED0004, (8192, 8192), 0.02)
-    blocks, scales = synth.mxfp4_quantize(Wm)
-    gemv_line(torch, q, lambda c: [q.QLinear.from_mxfp4(blocks, scales, 8192, 8192)
-                                   for _ in range(c)],
-              8192 * 4096 + 8192 * 256, [1, 16], torch.bfloat16, warmup, "mxfp4_8192_bf16", out)
-    qm = q.QLinear.from_mxfp4(blocks, scales, 8192, 8192)
-    gemm_line(torch, qm, 512, 8192, 8192, torch.bfloat16, warmup, "mxfp4_gemm_M512_bf16", out)
-    del qm
-    # config 3: prefill GEMM at M = 64, 512, 2048 (bf16): GPTQ, AWQ, GPTQ act-order
+    if "mxfp4" in only:
+        Wm = synth.normal(0x5EED0004, (8192, 8192), 0.02)
+        blocks, scales = synth.mxfp4_quantize(Wm)
+        gemv_line(torch, q, lambda c: [q.QLinear.from_mxfp4(blocks, scales, 8192, 8192)
+                                       for _ in range(c)],
+                  8192 * 4096 + 8192 * 256, [1, 16], torch.bfloat16, warmup, "mxfp4_8192_bf16",
+                  out)
+        qm = q.QLinear.from_mxfp4(blocks, scales, 8192, 8192)
+        gemm_line(torch, qm, 512, 8192, 8192, torch.bfloat16, warmup, "mxfp4_gemm_M512_bf16",
+                  out)
+        del qm
+    if "gemm" in only:
+        gemm_configs(torch, q, warmup, out)
+    if "moe" in only:
+        moe_configs(torch, q, warmup, out)
+    return out
+
+
+def gemm_configs(torch, q, warmup, out):
+    """config 3: prefill GEMM at M = 64, 512, 2048 (bf16): GPTQ, AWQ, GPTQ act-order"""
+    import synth
     w = gptq_weight(11008, 4096, 0x5EED0002)
     ql = make_gptq(q, w, 11008, 4096, 1)[0]
     for M in (64, 512, 2048):
@@ -207,7 +225,12 @@ def extra_configs(torch, q, warmup):
     gemm_line(torch, qx, 512, 4096, 11008, torch.bfloat16, warmup, "gptq_actorder_gemm_M512_bf16",
               out)
     del qx
-    # config 5: DeepSeek-style routed MoE, 64 experts, hidden 2048, inter 1408, top-6
+
+
+def moe_configs(torch, q, warmup, out):
+    """config 5: DeepSeek-style routed MoE, 64 experts, hidden 2048, inter 1408, top-6"""
+    import numpy as np
+    import synth
     n_exp, E, mi, k = 64, 2048, 1408, 6
     cfg = q.make_cfg(method=2, bits=4, group_size=128, zero_point=1)
     gu, dn = [], []
@@ -249,6 +272,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=24)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only", default=",".join(EXTRA_SECTIONS),
+                    help="comma-separated extra sections: " + ", ".join(EXTRA_SECTIONS))
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (the reference kernel of known "
@@ -321,7 +346,7 @@ def main():
     }
     if not args.no_extra:
         try:
-            res["extra"] = extra_configs(torch, q, 2)
+            res["extra"] = extra_configs(torch, q, 2, tuple(args.only.split(",")))
         except Exception as ex:  # secondary numbers must not hide the headline
             res["extra"] = {"error": repr(ex)}
     if not args.no_cpu:
