@@ -1,19 +1,19 @@
 // gemm.hip — prefill-side quantized linear, C[M,N] = A[M,K] * W^T (+ bias) for M > 16.
 //
-// Two launches:
-//   k_prep_a  one workgroup per row: finds the row's largest |a|, scales the row by an exact
-//             power of two into f16 range and writes it as MFMA A operands (f16 hi, plus lo
-//             for f32 inputs) in the layout [piece][step][kq][Mpad][8], gathering through kmap
-//             (act-order) on the way; rows M..Mpad are zero.
-//   k_gemm    128 x BN output tile per workgroup of 4 waves (2 x 2, each 64 x BN/2).  Per K
-//             chunk the workgroup copies the A operands of its 128 rows to LDS (double-buffered,
-//             the next chunk's global loads in flight during the current chunk's MFMAs), while
-//             every wave loads its own weight codes straight into registers (one 128-bit load
-//             per lane per 16-column tile), unpacks them into exact f16 (q - z) and runs
-//             v_mfma_f32_16x16x32_f16.  Group scales are applied in fp32 once per chunk; MXFP4
-//             block scales are folded into the fp4 -> f16 conversion relative to a per-column
-//             exponent (exact for every block within 2^23 of the column's largest), which is
-//             applied at the end.
+// Launches:
+//   k_rowexp + k_prep_a  the A operands, once per call: per row an exact power of two that puts
+//             max|a| in [2^13, 2^14), then f16 hi (+ lo for f32 inputs) in the layout
+//             [piece][step][kq][Mpad][8], gathered through kmap (act-order); rows M..Mpad are
+//             zero.
+//   k_gemm_lds  weights whose codes prescale exactly enough into f16 (groups with f16 scales in
+//             [2^-14, 128], and MXFP4): each workgroup unpacks its weight tile once per stage
+//             into LDS next to the A operands, through a ring of LDS buffers, and its waves run
+//             v_mfma_f32_16x16x32_f16 from there.  Small M splits the stages over K, and
+//             k_splitk_reduce adds the slices in order.
+//   k_gemm    every other weight: each wave loads its own codes straight into registers,
+//             unpacks exact f16 (q - z) and applies the group scales in fp32 per chunk or step.
+// MXFP4 block scales are folded into the fp4 -> f16 conversion relative to a per-column
+// exponent (exact for every block within 2^23 of the column's largest), applied at the end.
 #include <stdlib.h>
 #include <string.h>
 
