@@ -159,11 +159,16 @@ __device__ __forceinline__ void decode_meta(meta_t<SCF16> m, float &sc, half2_t 
 // element i of a U4 operand holds k-offset {0,4,1,5,2,6,3,7}[i]
 __device__ __forceinline__ constexpr int kofs4(int i) { return (i >> 1) + 4 * (i & 1); }
 
-template <int KIND, int CPW, bool SPLIT, bool SCF16, bool STEPM, bool FAST>
+// SPL: 0 = 16-bit activations (one f16 part); 1 = f32 activations as f16 hi + lo, two MFMAs per
+// step; 2 = f32 activations with at most 8 rows: the lo rows sit right below the hi rows in the
+// staging area (rows M .. 2M-1), so one MFMA covers both and row r + M is added to row r at the
+// end.
+template <int KIND, int CPW, int SPL, bool SCF16, bool STEPM, bool FAST>
 __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
   constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
-  constexpr int NP = SPLIT ? 2 : 1;
+  constexpr bool SPLIT = SPL != 0, FOLD = SPL == 2;
+  constexpr int NP = SPL == 1 ? 2 : 1;  // MFMAs per step
   constexpr int RW = SPLIT ? 2 : 1;  // 128-bit words per 8-element activation item
   constexpr int KEEP = 2;            // items per thread held in registers across the passes
   extern __shared__ half8_t s_act[];  // [NP][M][RS] activation operands, then [waves][64] acc
@@ -345,12 +350,12 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   // with a zero scale, which keeps the code straight-line and every load ahead of its use.
   // Lanes of rows >= M read row M-1 instead: an A row only feeds the same row of the
   // product, and rows >= M are never written.
-  const half8_t *arow_p = s_act + min(n16, M - 1) * RS + ks * CPW * SPC * 4 + kq;
+  const half8_t *arow_p = s_act + min(n16, (FOLD ? 2 * M : M) - 1) * RS + ks * CPW * SPC * 4 + kq;
   auto read_ops = [&](int i, half8_t (&op)[SPC * NP]) {
 #pragma unroll
     for (int j = 0; j < SPC; j++) {
       op[j] = arow_p[(i * SPC + j) * 4];
-      if constexpr (SPLIT) op[SPC + j] = arow_p[M * RS + (i * SPC + j) * 4];
+      if constexpr (NP == 2) op[SPC + j] = arow_p[M * RS + (i * SPC + j) * 4];
     }
   };
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -377,7 +382,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
       // even and odd chunks accumulate in separate registers: two independent MFMA chains
       float4_t &tc = pacc[i & 1];
       tc = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[j], b, tc, 0, 0, 0);
-      if constexpr (SPLIT)
+      if constexpr (NP == 2)
         tc = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[SPC + j], b, tc, 0, 0, 0);
       if constexpr (E2M1 || STEPM) {
         if constexpr (E2M1) {
@@ -405,6 +410,19 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
     if (ks != 0) return;
     acc = red[w * 64 + lane];
     for (int q = 1; q < a.ks; q++) acc += red[(w + q) * 64 + lane];
+  }
+
+  if constexpr (FOLD) {
+    // row r (hi part) += row r + M (lo part); row rr of this column sits in lane
+    // 16 (rr / 4) + n16, element rr % 4, and (i + M) % 4 is the same for every lane
+    float4_t f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int pr = 4 * kq + i + M, e = (i + M) & 3;
+      const float v = e == 0 ? acc[0] : e == 1 ? acc[1] : e == 2 ? acc[2] : acc[3];
+      f[i] = acc[i] + __shfl(v, ((pr >> 2) & 3) * 16 + n16);
+    }
+    acc = f;
   }
 
   // lane holds rows 4*kq + i of column n (v_mfma_f32_16x16x32 C layout)
@@ -483,22 +501,22 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   if (tid == 0) __hip_atomic_store(&a.cnt[cg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int KIND, int CPW, bool SPLIT, bool FAST>
+template <int KIND, int CPW, int SPL, bool FAST>
 void launch4(const GemvArgs &a, int scf16, int stepm, size_t lds, dim3 grid, unsigned nthr,
              hipStream_t st) {
   if constexpr (KIND == SGLQ_KIND_E2M1) {
-    k_gemv<KIND, CPW, SPLIT, true, false, FAST><<<grid, nthr, lds, st>>>(a);
+    k_gemv<KIND, CPW, SPL, true, false, FAST><<<grid, nthr, lds, st>>>(a);
   } else {
     if (scf16) {
       if (stepm)
-        k_gemv<KIND, CPW, SPLIT, true, true, FAST><<<grid, nthr, lds, st>>>(a);
+        k_gemv<KIND, CPW, SPL, true, true, FAST><<<grid, nthr, lds, st>>>(a);
       else
-        k_gemv<KIND, CPW, SPLIT, true, false, FAST><<<grid, nthr, lds, st>>>(a);
+        k_gemv<KIND, CPW, SPL, true, false, FAST><<<grid, nthr, lds, st>>>(a);
     } else {
       if (stepm)
-        k_gemv<KIND, CPW, SPLIT, false, true, FAST><<<grid, nthr, lds, st>>>(a);
+        k_gemv<KIND, CPW, SPL, false, true, FAST><<<grid, nthr, lds, st>>>(a);
       else
-        k_gemv<KIND, CPW, SPLIT, false, false, FAST><<<grid, nthr, lds, st>>>(a);
+        k_gemv<KIND, CPW, SPL, false, false, FAST><<<grid, nthr, lds, st>>>(a);
     }
   }
 }
@@ -506,16 +524,22 @@ void launch4(const GemvArgs &a, int scf16, int stepm, size_t lds, dim3 grid, uns
 template <int KIND, int CPW>
 void launch_cpw(const GemvArgs &a, bool split, int scf16, int stepm, bool fast, size_t lds,
                 dim3 grid, unsigned nthr, hipStream_t st) {
-  if (split) {
+  // f32 activations of at most 8 rows: hi and lo parts share one MFMA
+  if (split && a.M <= 8) {
     if (fast)
-      launch4<KIND, CPW, true, true>(a, scf16, stepm, lds, grid, nthr, st);
+      launch4<KIND, CPW, 2, true>(a, scf16, stepm, lds, grid, nthr, st);
     else
-      launch4<KIND, CPW, true, false>(a, scf16, stepm, lds, grid, nthr, st);
+      launch4<KIND, CPW, 2, false>(a, scf16, stepm, lds, grid, nthr, st);
+  } else if (split) {
+    if (fast)
+      launch4<KIND, CPW, 1, true>(a, scf16, stepm, lds, grid, nthr, st);
+    else
+      launch4<KIND, CPW, 1, false>(a, scf16, stepm, lds, grid, nthr, st);
   } else {
     if (fast)
-      launch4<KIND, CPW, false, true>(a, scf16, stepm, lds, grid, nthr, st);
+      launch4<KIND, CPW, 0, true>(a, scf16, stepm, lds, grid, nthr, st);
     else
-      launch4<KIND, CPW, false, false>(a, scf16, stepm, lds, grid, nthr, st);
+      launch4<KIND, CPW, 0, false>(a, scf16, stepm, lds, grid, nthr, st);
   }
 }
 
