@@ -103,6 +103,25 @@ _destroy = _sig("sgl_qlinear_destroy", None, _P)
 _moe = _sig("sgl_qmoe_forward", _I, _P, _P, _I, _P, _I, _I64, _P, _P, _I, _P, _P)
 
 
+class QLoadInfo(C.Structure):
+    _fields_ = [("kind", C.c_int), ("N", C.c_int64), ("K", C.c_int64), ("transposed", C.c_int),
+                ("layout", C.c_int)]
+
+
+QLOAD_KINDS = {0: "natural", 1: "marlin", 2: "ct", 3: "mxfp4"}
+_RAWFN = C.CFUNCTYPE(C.c_int, _P, C.c_char_p, C.POINTER(C.c_char_p), C.POINTER(C.c_int),
+                     C.POINTER(C.c_int64), C.POINTER(C.c_void_p), C.POINTER(C.c_size_t))
+_qst_open = _sig("sgl_qst_open", _P, C.c_char_p)
+_qst_raw = _sig("sgl_qst_get_raw", _I, _P, C.c_char_p, C.POINTER(C.c_char_p), C.POINTER(C.c_int),
+                C.POINTER(C.c_int64), C.POINTER(C.c_void_p), C.POINTER(C.c_size_t))
+_qst_close = _sig("sgl_qst_close", None, _P)
+_qst_raw_fn = C.cast(_qst_raw, _RAWFN)  # the reader's own lookup, passed to load / probe
+_probe = _sig("sgl_qlinear_probe", _I, C.POINTER(QCfg), _RAWFN, _P, C.c_char_p,
+              C.POINTER(QLoadInfo))
+_load = _sig("sgl_qlinear_load", _P, C.POINTER(QCfg), _RAWFN, _P, C.c_char_p,
+             C.POINTER(C.c_int64), C.POINTER(C.c_int64), _I)
+
+
 def _np(a, dt):
     return None if a is None else np.ascontiguousarray(a, dtype=dt)
 
@@ -219,6 +238,43 @@ def _dtype_code(t):
     return m[t.dtype]
 
 
+class SafeTensors:
+    """A single safetensors file opened by the library's reader (sgl_qst_*)."""
+
+    def __init__(self, path):
+        self.h = C.c_void_p(_qst_open(str(path).encode()))
+        if not self.h:
+            raise RuntimeError(f"sgl_qst_open({path}) failed (see the log line above)")
+
+    def get_raw(self, name):
+        """(dtype, dims, bytes) of a tensor, or None when the file has none by that name."""
+        dt, nd, dims = C.c_char_p(), C.c_int(), (C.c_int64 * 4)()
+        ptr, nb = C.c_void_p(), C.c_size_t()
+        if not _qst_raw(self.h, name.encode(), C.byref(dt), C.byref(nd), dims, C.byref(ptr),
+                        C.byref(nb)):
+            return None
+        data = C.string_at(ptr.value, nb.value) if nb.value else b""
+        return dt.value.decode(), tuple(dims[i] for i in range(nd.value)), data
+
+    def probe(self, cfg, base):
+        """(rc, info): rc 1 = loadable, 0 = no quantized tensors, -1 = error."""
+        info = QLoadInfo()
+        rc = _probe(C.byref(cfg), _qst_raw_fn, self.h, base.encode(), C.byref(info))
+        return rc, {"kind": QLOAD_KINDS.get(info.kind), "N": info.N, "K": info.K,
+                    "transposed": info.transposed, "layout": info.layout}
+
+    def close(self):
+        if self.h:
+            _qst_close(self.h)
+            self.h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class QLinear:
     """A quantized weight resident on the GPU (sgl_qlinear)."""
 
@@ -252,6 +308,12 @@ class QLinear:
     def from_mxfp4(cls, blocks, scales, N, K, dev=0):
         wp, sc = _np(blocks, np.uint8), _np(scales, np.uint8)
         return cls(_create_mx(_ptr(wp), *_shape2(wp), _ptr(sc), *_shape2(sc), N, K, dev))
+
+    @classmethod
+    def load(cls, cfg, st, base, dev=0):
+        """sgl_qlinear_load from a SafeTensors reader: the tensors under `base` as the
+        reference's quant_get finds them.  cfg.transposed may be set (AWQ gemv layout)."""
+        return cls(_load(C.byref(cfg), _qst_raw_fn, st.h, base.encode(), None, None, dev))
 
     @classmethod
     def from_w8(cls, W8, sw, dev=0):
