@@ -15,7 +15,8 @@
  *   checking: sgl_qlinear_dequant  writes that W (f32 [N,K]) to device memory, bit-identical
  *             to the reference dequant.
  *   MoE:      sgl_qmoe_forward     routed expert FFN with the weighted combine of reference
- *             src/deepseek.c:655-677 (routing itself is an input).
+ *             src/deepseek.c:655-677; sgl_qmoe_router_logits + sgl_qmoe_route compute its
+ *             routing (:593-633) and sgl_qmoe_shared adds the shared experts (:679-687).
  *
  * All pointers passed to create* are host pointers.  Pointers passed to forward/dequant/moe are
  * device pointers; `stream` is a hipStream_t (NULL = default stream).  A handle is bound to
@@ -88,6 +89,37 @@ void sgl_qlinear_destroy(sgl_qlinear *ql);
 int sgl_qmoe_forward(sgl_qlinear *const *gate_up, sgl_qlinear *const *down, int n_experts,
                      const void *h, int h_dtype, int64_t T, const int32_t *topk_ids,
                      const float *topk_w, int k, float *out, void *stream);
+
+/* Routing of one MoE block on the device (reference src/deepseek.c:593-633; with
+ * sgl_qmoe_router_logits, sgl_qmoe_forward and sgl_qmoe_shared the whole block runs on one
+ * stream with no host synchronisation). */
+typedef struct {
+  int sigmoid;        /* 1: sigmoid scores (scoring_func "sigmoid"), 0: softmax */
+  int n_group;        /* > 1: group_limited_greedy over n_group equal groups of experts */
+  int topk_group;     /* groups kept (1 .. n_group) */
+  int k;              /* experts per token */
+  int norm_topk;      /* norm_topk_prob: weights / (their sum + 1e-20) when k > 1 */
+  float routed_scale; /* routed_scaling_factor */
+} sgl_qmoe_routing;
+
+/* logits[t][e] = h_t . router_w[e]: the router product (reference :594, sgl_matmul_nt on the
+ * f32 router weight); router_w f32 [n_experts, E], h [T, E] (h_dtype), logits f32 [T,
+ * n_experts], all device memory.  fp32 accumulation in another order than the reference's, so
+ * logits agree to rounding, not bit for bit.  E at most 16384. */
+int sgl_qmoe_router_logits(const float *router_w, int n_experts, const void *h, int h_dtype,
+                           int64_t T, int64_t E, float *logits, void *stream);
+
+/* topk_ids int32 [T, k] and topk_w f32 [T, k] from the logits: scores, e_bias (the
+ * e_score_correction_bias, may be NULL) added for the choice only, group-limited greedy choice,
+ * top-k with ties to the lower index (-1 with weight 0 when fewer than k experts remain),
+ * weights from the uncorrected scores.  At most 256 experts and 64 groups. */
+int sgl_qmoe_route(const sgl_qmoe_routing *r, const float *logits, const float *e_bias,
+                   int n_experts, int64_t T, int32_t *topk_ids, float *topk_w, void *stream);
+
+/* out[t] += the shared experts' SwiGLU MLP of h_t (reference :679-687, added after the routed
+ * sum): gate_up [2*sh, E] (gate rows, then up rows), down [E, sh]. */
+int sgl_qmoe_shared(sgl_qlinear *gate_up, sgl_qlinear *down, const void *h, int h_dtype,
+                    int64_t T, float *out, void *stream);
 
 #ifdef __cplusplus
 }

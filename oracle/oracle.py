@@ -181,6 +181,34 @@ class Oracle(_Lib):
         self._moe.argtypes = [_P, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, C.c_int, _P]
         self._moe.restype = None
         self.lib.orc_num_threads.restype = C.c_int
+        self._route = self.lib.orc_moe_route
+        self._route.argtypes = [_P, C.c_int, C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int,
+                                C.c_int, C.c_float, _P, _P]
+        self._route.restype = None
+        self._shared = self.lib.orc_moe_shared
+        self._shared.argtypes = [_P, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P]
+        self._shared.restype = None
+
+    def moe_route(self, logits, k, bias=None, sigmoid=True, n_group=0, topk_group=0,
+                  norm=True, scale=1.0):
+        """logits f32 [T, n_experts] -> (ids int32 [T, k], weights f32 [T, k])."""
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        T, ne = lg.shape
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        ids = np.zeros((T, k), np.int32)
+        w = np.zeros((T, k), np.float32)
+        self._route(_ptr(lg), T, ne, _ptr(b), int(sigmoid), n_group, topk_group, k, int(norm),
+                    scale, _ptr(ids), _ptr(w))
+        return ids, w
+
+    def moe_shared(self, h, wg, wu, wd, out):
+        """out += shared SwiGLU MLP of h (in place); wg/wu [sh, E], wd [E, sh]."""
+        h = np.ascontiguousarray(h, dtype=np.float32)
+        T, E = h.shape
+        wg, wu, wd = (np.ascontiguousarray(x, dtype=np.float32) for x in (wg, wu, wd))
+        assert out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
+        self._shared(_ptr(h), T, E, wg.shape[0], _ptr(wg), _ptr(wu), _ptr(wd), _ptr(out))
+        return out
 
     def num_threads(self):
         return self.lib.orc_num_threads()

@@ -18,6 +18,9 @@
  *   orc_quant_row(s)_i8       golden vectors + round-half-away / clamp / zero-row edge cases
  *   orc_matmul_w8a16/_nt      golden vectors (bit-exact) + fp64 brute-force dot (tolerance)
  *   orc_moe_ffn               brute-force composition in float64 on tiny expert sets
+ *   orc_moe_route             an independent numpy formulation (sorts and masks) on random
+ *                             logits, plus hand-built ties, masked groups and k = 1 cases
+ *   orc_moe_shared            float64 brute force of the shared SwiGLU MLP
  */
 #include <math.h>
 #include <stdint.h>
@@ -368,6 +371,124 @@ void orc_moe_ffn(const float *h, int T, int E, int mi, const float *const *w_gu,
     }
   }
   free(gu);
+  free(o);
+}
+
+/* Routing of one MoE block, following reference src/deepseek.c:593-633 for each token row of
+ * logits ([T][ne], the router product): scores s = sigmoid(logit) (sigmoid = 1) or the softmax
+ * of reference src/ops.c:220-231; selection scores ch = s + bias (bias may be NULL); with
+ * n_group > 1 (group_limited_greedy), group score = top-1 + top-2 of its ch, the topk_group
+ * best groups kept greedily (strictly greater wins, so ties go to the lower index), ch of the
+ * others set to -1e30; top-k over ch by the same greedy rule (-1 when nothing beats -1e30);
+ * weights = the uncorrected s of the chosen experts, normalised by their double sum + 1e-20
+ * when norm && k > 1, then times scale. */
+void orc_moe_route(const float *logits, int T, int ne, const float *bias, int sigmoid,
+                   int n_group, int topk_group, int k, int norm, float scale, int32_t *ids,
+                   float *wts) {
+  float *s = (float *)malloc(sizeof(float) * (size_t)ne);
+  float *ch = (float *)malloc(sizeof(float) * (size_t)ne);
+  float *gs = (float *)malloc(sizeof(float) * (size_t)(n_group > 0 ? n_group : 1));
+  int *gsel = (int *)malloc(sizeof(int) * (size_t)(n_group > 0 ? n_group : 1));
+  for (int t = 0; t < T; t++) {
+    memcpy(s, logits + (size_t)t * ne, sizeof(float) * (size_t)ne);
+    if (sigmoid) {
+      for (int i = 0; i < ne; i++) s[i] = 1.0f / (1.0f + expf(-s[i]));
+    } else {
+      float maxv = s[0];
+      for (int i = 1; i < ne; i++)
+        if (s[i] > maxv) maxv = s[i];
+      double sum = 0;
+      for (int i = 0; i < ne; i++) {
+        s[i] = expf(s[i] - maxv);
+        sum += s[i];
+      }
+      const float inv = (float)(1.0 / sum);
+      for (int i = 0; i < ne; i++) s[i] *= inv;
+    }
+    for (int i = 0; i < ne; i++) ch[i] = s[i] + (bias ? bias[i] : 0.0f);
+    if (n_group > 1) {
+      const int epg = ne / n_group;
+      for (int g = 0; g < n_group; g++) {
+        const float *b = ch + (size_t)g * epg;
+        float t1 = -1e30f, t2 = -1e30f;
+        for (int i = 0; i < epg; i++) {
+          if (b[i] > t1) {
+            t2 = t1;
+            t1 = b[i];
+          } else if (b[i] > t2) {
+            t2 = b[i];
+          }
+        }
+        gs[g] = epg > 1 ? t1 + t2 : t1;
+      }
+      for (int g = 0; g < n_group; g++) {
+        int best = -1;
+        float bv = -1e30f;
+        for (int i = 0; i < n_group; i++) {
+          int used = 0;
+          for (int j = 0; j < g; j++) used |= gsel[j] == i;
+          if (!used && gs[i] > bv) {
+            bv = gs[i];
+            best = i;
+          }
+        }
+        gsel[g] = best;
+      }
+      for (int i = 0; i < ne; i++) {
+        int keep = 0;
+        for (int j = 0; j < topk_group; j++) keep |= gsel[j] == i / epg;
+        if (!keep) ch[i] = -1e30f;
+      }
+    }
+    int32_t *sel = ids + (size_t)t * k;
+    float *sw = wts + (size_t)t * k;
+    for (int j = 0; j < k; j++) {
+      int best = -1;
+      float bv = -1e30f;
+      for (int i = 0; i < ne; i++) {
+        int used = 0;
+        for (int q = 0; q < j; q++) used |= sel[q] == i;
+        if (!used && ch[i] > bv) {
+          bv = ch[i];
+          best = i;
+        }
+      }
+      sel[j] = best;
+      sw[j] = best >= 0 ? s[best] : 0.0f;
+    }
+    if (k > 1 && norm) {
+      double tot = 0;
+      for (int j = 0; j < k; j++) tot += sw[j];
+      tot += 1e-20;
+      if (tot != 0)
+        for (int j = 0; j < k; j++) sw[j] = (float)(sw[j] / tot);
+    }
+    for (int j = 0; j < k; j++) sw[j] *= scale;
+  }
+  free(s);
+  free(ch);
+  free(gs);
+  free(gsel);
+}
+
+/* Shared experts of one MoE block, added after the routed sum as reference
+ * src/deepseek.c:679-687: out_t += (silu(h_t Wg^T) * (h_t Wu^T)) Wd^T, Wg/Wu [sh][E], Wd [E][sh],
+ * each product by orc_matmul_nt (the reference's sgl_matmul_nt). */
+void orc_moe_shared(const float *h, int T, int E, int sh, const float *wg, const float *wu,
+                    const float *wd, float *out) {
+  float *g = (float *)malloc(sizeof(float) * (size_t)sh);
+  float *u = (float *)malloc(sizeof(float) * (size_t)sh);
+  float *o = (float *)malloc(sizeof(float) * (size_t)E);
+  for (int t = 0; t < T; t++) {
+    orc_matmul_nt(h + (size_t)t * E, wg, NULL, g, 1, sh, E);
+    orc_matmul_nt(h + (size_t)t * E, wu, NULL, u, 1, sh, E);
+    for (int i = 0; i < sh; i++) g[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+    orc_matmul_nt(g, wd, NULL, o, 1, E, sh);
+    float *orow = out + (size_t)t * E;
+    for (int i = 0; i < E; i++) orow[i] += o[i];
+  }
+  free(g);
+  free(u);
   free(o);
 }
 

@@ -488,6 +488,7 @@ extern "C" void sglq_free(sglq_dev *d) {
   (void)hipFree(d->kmap);
   (void)hipFree(d->kinv);
   (void)hipFree(d->ws);
+  (void)hipFree(d->aux);
   free(d->moe_tbl);
   free(d);
 }
@@ -502,6 +503,19 @@ int sglq_ws_reserve(sglq_dev *d, size_t bytes) {
     return -1;
   }
   d->ws_bytes = bytes;
+  return 0;
+}
+
+int sglq_aux_reserve(sglq_dev *d, size_t bytes) {
+  if (d->aux_bytes >= bytes) return 0;
+  (void)hipFree(d->aux);
+  d->aux = nullptr;
+  d->aux_bytes = 0;
+  if (hipMalloc(&d->aux, bytes) != hipSuccess) {
+    sglq_log_error("auxiliary buffer allocation of %zu bytes failed", bytes);
+    return -1;
+  }
+  d->aux_bytes = bytes;
   return 0;
 }
 

@@ -60,6 +60,10 @@ struct sglq_dev {
   // prefill GEMM / MoE workspace (grown on demand)
   void *ws;
   size_t ws_bytes;
+  // buffers of an MoE shared-expert pass owned by its gate/up handle (grown on demand; apart
+  // from ws, which the forwards inside that pass use)
+  void *aux;
+  size_t aux_bytes;
   // MoE: host copy of the expert pointer table last uploaded into ws (re-uploaded on change)
   void *moe_tbl;
   size_t moe_tbl_bytes;
@@ -81,6 +85,7 @@ static inline unsigned sglq_blocks(int64_t n, int threads) {
 }
 
 // Grows d->ws to at least `bytes` (device memory, kept for the handle's lifetime).
+int sglq_aux_reserve(sglq_dev *d, size_t bytes);
 int sglq_ws_reserve(sglq_dev *d, size_t bytes);
 
 // Decode-GEMV launch (gemv.hip): C rows [0, M) with M <= 16.

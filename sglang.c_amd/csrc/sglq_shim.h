@@ -91,6 +91,15 @@ int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down, int n_exp,
                      int h_dtype, int64_t T, const int32_t *topk_ids, const float *topk_w,
                      int k, float *out, void *stream);
 
+/* MoE routing and shared experts on the device (route.hip; see sgl_qmoe_route). */
+int sglq_moe_router_logits(const float *router_w, int ne, const void *h, int h_dtype, int64_t T,
+                           int64_t E, float *logits, void *stream);
+int sglq_moe_route(const float *logits, int64_t T, int ne, const float *bias, int sigmoid,
+                   int n_group, int topk_group, int k, int norm, float scale, int32_t *ids,
+                   float *wts, void *stream);
+int sglq_moe_shared(sglq_dev *gate_up, sglq_dev *down, const void *h, int h_dtype, int64_t T,
+                    float *out, void *stream);
+
 /* Logging hook implemented by the host layer. */
 void sglq_log_error(const char *fmt, ...);
 

@@ -524,6 +524,35 @@ QH_API int sgl_qmoe_forward(sgl_qlinear *const *gate_up, sgl_qlinear *const *dow
   return rc;
 }
 
+QH_API int sgl_qmoe_router_logits(const float *router_w, int n_experts, const void *h,
+                                  int h_dtype, int64_t T, int64_t E, float *logits,
+                                  void *stream) {
+  if (!router_w || !h || !logits || T < 0) return -1;
+  if (h_dtype != SGL_QL_F32 && h_dtype != SGL_QL_BF16 && h_dtype != SGL_QL_F16) {
+    QH_ERR("qmoe router: unknown activation dtype %d", h_dtype);
+    return -1;
+  }
+  return sglq_moe_router_logits(router_w, n_experts, h, h_dtype, T, E, logits, stream);
+}
+
+QH_API int sgl_qmoe_route(const sgl_qmoe_routing *r, const float *logits, const float *e_bias,
+                          int n_experts, int64_t T, int32_t *topk_ids, float *topk_w,
+                          void *stream) {
+  if (!r || !logits || !topk_ids || !topk_w || T < 0) return -1;
+  return sglq_moe_route(logits, T, n_experts, e_bias, r->sigmoid, r->n_group, r->topk_group,
+                        r->k, r->norm_topk, r->routed_scale, topk_ids, topk_w, stream);
+}
+
+QH_API int sgl_qmoe_shared(sgl_qlinear *gate_up, sgl_qlinear *down, const void *h, int h_dtype,
+                           int64_t T, float *out, void *stream) {
+  if (!gate_up || !down || !h || !out || T < 0) return -1;
+  if (h_dtype != SGL_QL_F32 && h_dtype != SGL_QL_BF16 && h_dtype != SGL_QL_F16) {
+    QH_ERR("qmoe shared: unknown activation dtype %d", h_dtype);
+    return -1;
+  }
+  return sglq_moe_shared(gate_up->d, down->d, h, h_dtype, T, out, stream);
+}
+
 /* ---- config.json quantization_config (reference src/qweight.c:375-482) ---------------- */
 QH_API int sgl_qcfg_from_json(const char *json, size_t len, sgl_qcfg *cfg) {
   if (!cfg) return 0;

@@ -376,3 +376,51 @@ def qmoe_forward(gate_up, down, h, topk_ids, topk_w, out=None):
     if rc != 0:
         raise RuntimeError("sgl_qmoe_forward failed")
     return out
+
+
+class QMoERouting(C.Structure):
+    _fields_ = [("sigmoid", C.c_int), ("n_group", C.c_int), ("topk_group", C.c_int),
+                ("k", C.c_int), ("norm_topk", C.c_int), ("routed_scale", C.c_float)]
+
+
+_router = _sig("sgl_qmoe_router_logits", _I, _P, _I, _P, _I, _I64, _I64, _P, _P)
+_route = _sig("sgl_qmoe_route", _I, C.POINTER(QMoERouting), _P, _P, _I, _I64, _P, _P, _P)
+_shared = _sig("sgl_qmoe_shared", _I, _P, _P, _P, _I, _I64, _P, _P)
+
+
+def qmoe_router_logits(router_w, h, out=None):
+    """router_w f32 [n_experts, E], h [T, E] device tensors -> logits f32 [T, n_experts]."""
+    import torch
+    w, h = router_w.contiguous(), h.contiguous()
+    T, E = h.shape
+    if out is None:
+        out = torch.empty((T, w.shape[0]), dtype=torch.float32, device=h.device)
+    if _router(C.c_void_p(w.data_ptr()), w.shape[0], C.c_void_p(h.data_ptr()), _dtype_code(h),
+               T, E, C.c_void_p(out.data_ptr()), _stream()) != 0:
+        raise RuntimeError("sgl_qmoe_router_logits failed")
+    return out
+
+
+def qmoe_route(logits, k, bias=None, sigmoid=True, n_group=0, topk_group=0, norm=True,
+               scale=1.0):
+    """logits f32 [T, n_experts] device tensor -> (topk_ids int32 [T, k], topk_w f32 [T, k])."""
+    import torch
+    lg = logits.contiguous()
+    T, ne = lg.shape
+    r = QMoERouting(int(sigmoid), n_group, topk_group, k, int(norm), scale)
+    ids = torch.empty((T, k), dtype=torch.int32, device=lg.device)
+    w = torch.empty((T, k), dtype=torch.float32, device=lg.device)
+    b = None if bias is None else bias.contiguous()
+    if _route(C.byref(r), C.c_void_p(lg.data_ptr()), None if b is None else C.c_void_p(b.data_ptr()),
+              ne, T, C.c_void_p(ids.data_ptr()), C.c_void_p(w.data_ptr()), _stream()) != 0:
+        raise RuntimeError("sgl_qmoe_route failed")
+    return ids, w
+
+
+def qmoe_shared(gate_up, down, h, out):
+    """out [T, E] f32 device tensor += the shared experts' SwiGLU MLP of h (in place)."""
+    h = h.contiguous()
+    if _shared(gate_up.h, down.h, C.c_void_p(h.data_ptr()), _dtype_code(h), h.shape[0],
+               C.c_void_p(out.data_ptr()), _stream()) != 0:
+        raise RuntimeError("sgl_qmoe_shared failed")
+    return out

@@ -1,0 +1,109 @@
+"""MoE routing and shared experts on the GPU against the oracle (orc_moe_route /
+orc_moe_shared restate reference src/deepseek.c:593-633 and :679-687).  Routing is compared on
+identical logits: the chosen experts must be identical, the weights agree to 2e-6 (the
+device's expf and the host's may differ in the last bit).  The router product is compared to
+the reference's sgl_matmul_nt within rounding."""
+import numpy as np
+import pytest
+
+import synth
+from linear_cases import rel_err
+from oracle.oracle import make_cfg as ocfg
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+@pytest.mark.parametrize("ne,k,sig,ng,tg,bias,norm", [
+    (64, 6, True, 8, 3, True, True), (64, 6, False, 0, 0, False, True),
+    (256, 8, True, 8, 4, True, True), (16, 1, True, 0, 0, False, True),
+    (32, 4, False, 4, 2, False, False), (8, 2, True, 8, 3, True, True), (160, 6, False, 0, 0,
+                                                                        False, False)])
+def test_route_matches_oracle(orc, ne, k, sig, ng, tg, bias, norm):
+    import sgl_qlinear as q
+    rng = np.random.default_rng(ne * 10 + k)
+    lg = (rng.standard_normal((96, ne)) * 2).astype(np.float32)
+    b = (rng.standard_normal(ne) * 0.1).astype(np.float32) if bias else None
+    print(f"[gpu] route ne={ne} k={k} sigmoid={sig} groups={ng}/{tg}", flush=True)
+    ids, w = q.qmoe_route(_dev(lg), k, None if b is None else _dev(b), sig, ng, tg, norm, 2.5)
+    rid, rw = orc.moe_route(lg, k, b, sig, ng, tg, norm, 2.5)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=2e-6, atol=0)
+
+
+def test_route_edge_cases(orc):
+    import sgl_qlinear as q
+    cases = [(np.array([[0.5, 1.0, 1.0, 0.2, 1.0, 1.0]], np.float32), 3, {}),
+             (np.array([[1.0, 1.0, 0.0, 0.0, 1.0, 1.0, 0.5, 0.5]], np.float32), 2,
+              dict(n_group=4, topk_group=1)),
+             (np.arange(16, dtype=np.float32)[None, :], 6, dict(n_group=4, topk_group=1)),
+             (np.array([[0.1, 3.0, 2.0, -1.0]], np.float32), 2, dict(n_group=4, topk_group=2))]
+    for lg, k, kw in cases:
+        ids, w = q.qmoe_route(_dev(lg), k, **kw)
+        rid, rw = orc.moe_route(lg, k, **kw)
+        assert np.array_equal(ids.cpu().numpy(), rid), (lg, kw)
+        np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=2e-6, atol=0)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_router_logits(orc, dt):
+    import torch
+    import sgl_qlinear as q
+    T, E, ne = 37, 2048, 64
+    h = synth.normal(3, (T, E))
+    w = synth.normal(4, (ne, E), 0.02)
+    if dt == "bf16":
+        h = synth.bf16_bits_to_f32(synth.to_bf16_bits(h))
+        th = _dev(h).to(torch.bfloat16)
+    else:
+        th = _dev(h)
+    got = q.qmoe_router_logits(_dev(w), th).cpu().numpy()
+    assert rel_err(got, orc.matmul_nt(h, w)) <= 1e-5
+
+
+def test_moe_block_end_to_end(orc):
+    """Router -> route -> routed experts -> shared experts, all on one stream, against the
+    oracle's composition (DeepSeek-V3-style: sigmoid, correction bias, 4 groups keep 2)."""
+    import torch
+    import sgl_qlinear as q
+    n_exp, E, mi, sh, k, T = 16, 256, 128, 256, 4, 24
+    cfg = dict(method=2, bits=4, group_size=128, zero_point=1)
+
+    def qlin(seed, N, K):
+        qw, qz, s = synth.gptq_expert(seed, N, K)
+        rc, W = orc.dequant(ocfg(**cfg), qw, s, N, K, qzeros=qz)
+        assert rc == 0
+        return q.QLinear.from_awq_gptq(q.make_cfg(**cfg), qw, s, N, K, qzeros=qz), W
+
+    gu, dn, wgu, wdn = [], [], [], []
+    for e in range(n_exp):
+        a, wa = qlin(100 + 2 * e, 2 * mi, E)
+        b, wb = qlin(101 + 2 * e, E, mi)
+        gu.append(a), dn.append(b), wgu.append(wa), wdn.append(wb)
+    sgu, wsgu = qlin(500, 2 * sh, E)
+    sdn, wsdn = qlin(501, E, sh)
+    router = synth.normal(7, (n_exp, E), 0.05)
+    bias = (np.random.default_rng(8).standard_normal(n_exp) * 0.05).astype(np.float32)
+    h = synth.normal(9, (T, E))
+    th = _dev(h)
+    logits = q.qmoe_router_logits(_dev(router), th)
+    ids, w = q.qmoe_route(logits, k, _dev(bias), True, 4, 2, True, 2.5)
+    out = q.qmoe_forward(gu, dn, th, ids, w)
+    q.qmoe_shared(sgu, sdn, th, out)
+    rid, rw = orc.moe_route(orc.matmul_nt(h, router), k, bias, True, 4, 2, True, 2.5)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    ref = orc.moe_ffn(h, wgu, wdn, rid, rw)
+    orc.moe_shared(h, wsgu[:sh], wsgu[sh:], wsdn, ref)
+    assert rel_err(out.cpu().numpy(), ref) <= 1e-3
+    # decode-sized batch through the same calls
+    t1 = th[:2].contiguous()
+    lg1 = q.qmoe_router_logits(_dev(router), t1)
+    i1, w1 = q.qmoe_route(lg1, k, _dev(bias), True, 4, 2, True, 2.5)
+    o1 = q.qmoe_forward(gu, dn, t1, i1, w1)
+    q.qmoe_shared(sgu, sdn, t1, o1)
+    assert rel_err(o1.cpu().numpy(), ref[:2]) <= 1e-3
+    torch.cuda.synchronize()
