@@ -121,6 +121,21 @@ int sgl_qmoe_route(const sgl_qmoe_routing *r, const float *logits, const float *
 int sgl_qmoe_shared(sgl_qlinear *gate_up, sgl_qlinear *down, const void *h, int h_dtype,
                     int64_t T, float *out, void *stream);
 
+/* Dense SwiGLU MLP of T rows (reference src/llama.c:1162-1176 mlp_rows with proj_nt):
+ * out = (silu(h gate^T) * (h up^T)) down^T, silu(g) = g / (1 + expf(-g)); up == NULL means gate
+ * is the fused [2*I, E] weight (gate rows, then up rows).  h [T, E] (h_dtype), out f32 [T, E]. */
+int sgl_qmlp_forward(sgl_qlinear *gate, sgl_qlinear *up, sgl_qlinear *down, const void *h,
+                     int h_dtype, int64_t T, float *out, void *stream);
+
+/* Device-pointer, stream-ordered twins of sgl_quant_rows_i8 / sgl_dequant_row_i8 (sgl/quant.h,
+ * same arithmetic, bit for bit): the int8 KV-cache rows quantized where they are produced
+ * (reference src/llama.c:1264-1267, 1485-1488).  x f32 [rows, dim] -> out int8 [rows, dim] +
+ * scales f32 [rows]; dequant: out[r][i] = q[r][i] * scales[r]. */
+int sgl_quant_rows_i8_dev(const float *x, int8_t *out, float *scales, int64_t rows, int64_t dim,
+                          void *stream);
+int sgl_dequant_rows_i8_dev(const int8_t *q, const float *scales, float *out, int64_t rows,
+                            int64_t dim, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

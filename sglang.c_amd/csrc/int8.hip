@@ -157,3 +157,33 @@ fail:
   (void)hipFree(dC);
   return -1;
 }
+
+// out[r][i] = (float)q[r][i] * scales[r]: sgl_dequant_row_i8 over rows
+__global__ void k_dequant_rows_i8(const int8_t *__restrict__ q, const float *__restrict__ sc,
+                                  float *__restrict__ o, int64_t rows, int64_t dim) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < rows * dim) o[i] = (float)q[i] * sc[i / dim];
+}
+
+// device-pointer variants (stream-ordered): the int8 KV-cache rows quantized where they are
+// produced (reference src/llama.c:1264-1267, 1485-1488 call sgl_quant_row_i8 on host rows)
+extern "C" int sglq_quant_rows_i8_dev(const float *x, int8_t *out, float *scales, int64_t rows,
+                                      int64_t dim, void *stream) {
+  if (rows <= 0 || dim <= 0) return 0;
+  k_quant_rows_i8<<<(unsigned)rows, 256, 0, (hipStream_t)stream>>>(x, out, scales, dim);
+  SGLQ_HIP(hipGetLastError());
+  return 0;
+fail:
+  return -1;
+}
+
+extern "C" int sglq_dequant_rows_i8_dev(const int8_t *q, const float *scales, float *out,
+                                        int64_t rows, int64_t dim, void *stream) {
+  if (rows <= 0 || dim <= 0) return 0;
+  k_dequant_rows_i8<<<sglq_blocks(rows * dim, 256), 256, 0, (hipStream_t)stream>>>(
+      q, scales, out, rows, dim);
+  SGLQ_HIP(hipGetLastError());
+  return 0;
+fail:
+  return -1;
+}

@@ -9,8 +9,9 @@
 //                    group-limited greedy group choice, top-k as k wave argmaxes (strictly
 //                    greater wins: ties go to the lower index, nothing at or below -1e30 is
 //                    chosen), weights from the uncorrected scores, normalised in slot order
-//   shared experts   gate/up forward, k_swiglu, down forward, k_add_into (out += shared, after
-//                    the routed sum as the reference adds it)
+//   SwiGLU MLP       gate/up forward(s), k_swiglu, down forward: the shared experts (added
+//                    after the routed sum, as the reference adds them) and the dense MLP block
+//                    (reference src/llama.c:1162-1176)
 #include <string.h>
 
 #include "sglq_dev.hpp"
@@ -191,13 +192,16 @@ __global__ __launch_bounds__(64) void k_moe_gate(const float *__restrict__ logit
   }
 }
 
-__global__ void k_swiglu(const float *__restrict__ gu, int64_t T, int64_t sh,
-                         float *__restrict__ act) {
+// act[t][c] = silu(g) * u with silu(g) = g / (1 + expf(-g)) rounded first, as the reference's
+// sgl_silu_inplace followed by the product (reference src/ops.c:288-293, src/llama.c:1172-1173)
+__global__ void k_swiglu(const float *__restrict__ g, int64_t ldg, const float *__restrict__ u,
+                         int64_t ldu, int64_t T, int64_t I, float *__restrict__ act) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= T * sh) return;
-  const int64_t t = i / sh, c = i - t * sh;
-  const float g = gu[t * 2 * sh + c];
-  act[i] = (g / (1.0f + expf(-g))) * gu[t * 2 * sh + sh + c];
+  if (i >= T * I) return;
+  const int64_t t = i / I, c = i - t * I;
+  const float x = g[t * ldg + c];
+  const float s = x / (1.0f + expf(-x));
+  act[i] = s * u[t * ldu + c];
 }
 
 __global__ void k_add_into(float *__restrict__ out, const float *__restrict__ o, int64_t n) {
@@ -245,30 +249,49 @@ fail:
   return -1;
 }
 
-extern "C" int sglq_moe_shared(sglq_dev *gu, sglq_dev *dn, const void *h, int h_dtype,
-                               int64_t T, float *out, void *stream) {
-  hipStream_t st = (hipStream_t)stream;
-  if (gu->N % 2 != 0 || dn->K != gu->N / 2 || dn->N != gu->K) {
-    sglq_log_error("qmoe shared: gate_up [%lld,%lld] / down [%lld,%lld] do not form a SwiGLU "
-                   "MLP", (long long)gu->N, (long long)gu->K, (long long)dn->N,
-                   (long long)dn->K);
+// SwiGLU MLP of T rows: down(silu(h gate^T) * (h up^T)).  up == nullptr: gate is the fused
+// [2 I, K] weight (gate rows, then up rows).  accumulate: out += MLP, else out = MLP.  The
+// intermediate buffers live in gate's aux buffer.
+static int swiglu_mlp(sglq_dev *gate, sglq_dev *up, sglq_dev *down, const void *h, int h_dtype,
+                      int64_t T, float *out, bool accumulate, hipStream_t st) {
+  const int64_t I = down->K, E = down->N;
+  const bool fused = up == nullptr;
+  if ((fused && gate->N != 2 * I) || (!fused && (gate->N != I || up->N != I || up->K != gate->K))
+      || gate->K != E) {
+    sglq_log_error("SwiGLU MLP: gate [%lld,%lld]%s / down [%lld,%lld] do not fit",
+                   (long long)gate->N, (long long)gate->K, fused ? " (fused gate/up)" : "",
+                   (long long)down->N, (long long)down->K);
     return -1;
   }
   if (T == 0) return 0;
-  const int64_t sh = dn->K, E = dn->N;
-  const size_t o_act = ((size_t)T * 2 * sh * 4 + 255) / 256 * 256;
-  const size_t o_o = o_act + ((size_t)T * sh * 4 + 255) / 256 * 256;
-  if (sglq_aux_reserve(gu, o_o + (size_t)T * E * 4) != 0) return -1;
-  float *g = (float *)gu->aux;
-  float *act = (float *)((char *)gu->aux + o_act);
-  float *o = (float *)((char *)gu->aux + o_o);
-  if (sglq_forward(gu, h, h_dtype, T, nullptr, g, stream) != 0) return -1;
-  k_swiglu<<<sglq_blocks(T * sh, 256), 256, 0, st>>>(g, T, sh, act);
+  const size_t o_act = ((size_t)T * 2 * I * 4 + 255) / 256 * 256;
+  const size_t o_o = o_act + ((size_t)T * I * 4 + 255) / 256 * 256;
+  if (sglq_aux_reserve(gate, o_o + (accumulate ? (size_t)T * E * 4 : 0)) != 0) return -1;
+  float *g = (float *)gate->aux;
+  float *u = fused ? g + I : g + T * I;
+  float *act = (float *)((char *)gate->aux + o_act);
+  float *o = accumulate ? (float *)((char *)gate->aux + o_o) : out;
+  if (sglq_forward(gate, h, h_dtype, T, nullptr, g, st) != 0) return -1;
+  if (!fused && sglq_forward(up, h, h_dtype, T, nullptr, u, st) != 0) return -1;
+  k_swiglu<<<sglq_blocks(T * I, 256), 256, 0, st>>>(g, fused ? 2 * I : I, u, fused ? 2 * I : I,
+                                                    T, I, act);
   SGLQ_HIP(hipGetLastError());
-  if (sglq_forward(dn, act, SGLQ_DT_F32, T, nullptr, o, stream) != 0) return -1;
-  k_add_into<<<sglq_blocks(T * E, 256), 256, 0, st>>>(out, o, T * E);
-  SGLQ_HIP(hipGetLastError());
+  if (sglq_forward(down, act, SGLQ_DT_F32, T, nullptr, o, st) != 0) return -1;
+  if (accumulate) {
+    k_add_into<<<sglq_blocks(T * E, 256), 256, 0, st>>>(out, o, T * E);
+    SGLQ_HIP(hipGetLastError());
+  }
   return 0;
 fail:
   return -1;
+}
+
+extern "C" int sglq_moe_shared(sglq_dev *gu, sglq_dev *dn, const void *h, int h_dtype,
+                               int64_t T, float *out, void *stream) {
+  return swiglu_mlp(gu, nullptr, dn, h, h_dtype, T, out, true, (hipStream_t)stream);
+}
+
+extern "C" int sglq_mlp_forward(sglq_dev *gate, sglq_dev *up, sglq_dev *down, const void *h,
+                                int h_dtype, int64_t T, float *out, void *stream) {
+  return swiglu_mlp(gate, up, down, h, h_dtype, T, out, false, (hipStream_t)stream);
 }

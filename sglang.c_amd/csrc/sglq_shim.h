@@ -100,6 +100,13 @@ int sglq_moe_route(const float *logits, int64_t T, int ne, const float *bias, in
 int sglq_moe_shared(sglq_dev *gate_up, sglq_dev *down, const void *h, int h_dtype, int64_t T,
                     float *out, void *stream);
 
+int sglq_mlp_forward(sglq_dev *gate, sglq_dev *up, sglq_dev *down, const void *h, int h_dtype,
+                     int64_t T, float *out, void *stream);
+int sglq_quant_rows_i8_dev(const float *x, int8_t *out, float *scales, int64_t rows,
+                           int64_t dim, void *stream);
+int sglq_dequant_rows_i8_dev(const int8_t *q, const float *scales, float *out, int64_t rows,
+                             int64_t dim, void *stream);
+
 /* Logging hook implemented by the host layer. */
 void sglq_log_error(const char *fmt, ...);
 

@@ -553,6 +553,28 @@ QH_API int sgl_qmoe_shared(sgl_qlinear *gate_up, sgl_qlinear *down, const void *
   return sglq_moe_shared(gate_up->d, down->d, h, h_dtype, T, out, stream);
 }
 
+QH_API int sgl_qmlp_forward(sgl_qlinear *gate, sgl_qlinear *up, sgl_qlinear *down,
+                            const void *h, int h_dtype, int64_t T, float *out, void *stream) {
+  if (!gate || !down || !h || !out || T < 0) return -1;
+  if (h_dtype != SGL_QL_F32 && h_dtype != SGL_QL_BF16 && h_dtype != SGL_QL_F16) {
+    QH_ERR("qmlp: unknown activation dtype %d", h_dtype);
+    return -1;
+  }
+  return sglq_mlp_forward(gate->d, up ? up->d : NULL, down->d, h, h_dtype, T, out, stream);
+}
+
+QH_API int sgl_quant_rows_i8_dev(const float *x, int8_t *out, float *scales, int64_t rows,
+                                 int64_t dim, void *stream) {
+  if (!x || !out || !scales || rows < 0 || dim < 0) return -1;
+  return sglq_quant_rows_i8_dev(x, out, scales, rows, dim, stream);
+}
+
+QH_API int sgl_dequant_rows_i8_dev(const int8_t *q, const float *scales, float *out,
+                                   int64_t rows, int64_t dim, void *stream) {
+  if (!q || !scales || !out || rows < 0 || dim < 0) return -1;
+  return sglq_dequant_rows_i8_dev(q, scales, out, rows, dim, stream);
+}
+
 /* ---- config.json quantization_config (reference src/qweight.c:375-482) ---------------- */
 QH_API int sgl_qcfg_from_json(const char *json, size_t len, sgl_qcfg *cfg) {
   if (!cfg) return 0;

@@ -424,3 +424,42 @@ def qmoe_shared(gate_up, down, h, out):
                C.c_void_p(out.data_ptr()), _stream()) != 0:
         raise RuntimeError("sgl_qmoe_shared failed")
     return out
+
+
+_mlp = _sig("sgl_qmlp_forward", _I, _P, _P, _P, _P, _I, _I64, _P, _P)
+_qrows_dev = _sig("sgl_quant_rows_i8_dev", _I, _P, _P, _P, _I64, _I64, _P)
+_dqrows_dev = _sig("sgl_dequant_rows_i8_dev", _I, _P, _P, _P, _I64, _I64, _P)
+
+
+def qmlp_forward(gate, up, down, h, out=None):
+    """Dense SwiGLU MLP of h [T, E] (device): up None means gate is the fused [2I, E] weight."""
+    import torch
+    h = h.contiguous()
+    if out is None:
+        out = torch.empty((h.shape[0], down.N), dtype=torch.float32, device=h.device)
+    if _mlp(gate.h, None if up is None else up.h, down.h, C.c_void_p(h.data_ptr()),
+            _dtype_code(h), h.shape[0], C.c_void_p(out.data_ptr()), _stream()) != 0:
+        raise RuntimeError("sgl_qmlp_forward failed")
+    return out
+
+
+def quant_rows_i8_dev(x):
+    """x f32 [rows, dim] device tensor -> (int8 [rows, dim], f32 scales [rows]) on the device."""
+    import torch
+    x = x.contiguous()
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    s = torch.empty(x.shape[0], dtype=torch.float32, device=x.device)
+    if _qrows_dev(C.c_void_p(x.data_ptr()), C.c_void_p(q.data_ptr()), C.c_void_p(s.data_ptr()),
+                  x.shape[0], x.shape[1], _stream()) != 0:
+        raise RuntimeError("sgl_quant_rows_i8_dev failed")
+    return q, s
+
+
+def dequant_rows_i8_dev(q, scales):
+    import torch
+    q, scales = q.contiguous(), scales.contiguous()
+    o = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    if _dqrows_dev(C.c_void_p(q.data_ptr()), C.c_void_p(scales.data_ptr()),
+                   C.c_void_p(o.data_ptr()), q.shape[0], q.shape[1], _stream()) != 0:
+        raise RuntimeError("sgl_dequant_rows_i8_dev failed")
+    return o
