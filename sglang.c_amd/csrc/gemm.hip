@@ -543,16 +543,15 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 // buffers.  Each stage's A operands are copied and its weight codes unpacked (each code once
 // per workgroup, not once per wave) into a buffer while the MFMAs read another one; blockIdx.y
 // selects a slice of the stages when the call is split over K.
-template <int KIND, int NP, int BN, int SSX, int WMW, int NBUF>
+template <int KIND, int NP, int BN, int SSX, int WMW, int NBUF, int MB, int RS>
 __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
   constexpr int SS = SSX < SPC ? SSX : SPC;  // MFMA steps per stage
   constexpr int HPC = SPC / SS;         // stages per chunk
   constexpr int NTH = 128 * WMW;        // threads: WMW waves along M x 2 along N
-  constexpr int BMR = 64 * WMW;
+  constexpr int BMR = 16 * MB * WMW;   // rows: WMW waves of MB 16-row blocks
   constexpr int NT16 = BN / 16;         // weight tiles per workgroup
   constexpr int TN = NT16 / 2;          // per wave
-  constexpr int MB = 4;
   constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
   constexpr int AITEMS = NP * SS * 4 * BMR;  // 16-B A items per stage
   constexpr int AIPT = AITEMS / NTH;
@@ -692,7 +691,7 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
   // all operands of one stage are read from LDS before its MFMAs, so the reads overlap each
   // other and the MFMAs wait once
   auto compute = [&](int buf) {
-    const half8_t *sa = s_a + buf * AITEMS + wm * 64 + n16;
+    const half8_t *sa = s_a + buf * AITEMS + wm * (16 * MB) + n16;
     const half8_t *sb = s_b + buf * BITEMS + wn * TN * SS * 64 + lane;
     half8_t bv[SS][TN], av[SS][NP][MB];
 #pragma unroll
@@ -722,6 +721,39 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
   // r + 2 and multiplies stage r, so the loads of a stage have a whole iteration in flight.
   // One barrier per iteration; the loop body is uniform (past the end it reloads the last
   // stage into a buffer nobody reads).
+  if constexpr (RS == 2) {
+    // Two register sets, two LDS buffers: iteration r loads stage r + 2 into one set while the
+    // other holds stage r + 1 (loaded one iteration earlier), multiplies stage r and then writes
+    // stage r + 1 into the other buffer, so each stage's loads have two iterations in flight.
+    // Unrolled by two so that each set is named at compile time.
+    half8_t a0[AIPT], a1[AIPT];
+    u32x4_t b0[PB], b1[PB];
+    MT mr0[PB], mr1[PB];
+    auto step = [&](int st, int p, half8_t(&al)[AIPT], u32x4_t(&bl)[PB], MT(&ml)[PB],
+                    const half8_t(&as)[AIPT], const u32x4_t(&bs)[PB], const MT(&ms)[PB]) {
+      const int nx = min(st + 2, st1 - 1);  // past the end: a harmless reload
+      load_a(nx, al);
+      load_b(nx, bl, ml);
+      __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the MFMAs
+      compute(p);
+      store_a(p ^ 1, as);
+      store_b(p ^ 1, bs, ms);
+      __syncthreads();
+    };
+    load_a(st0, a0);
+    load_b(st0, b0, mr0);
+    load_a(min(st0 + 1, st1 - 1), a1);
+    load_b(min(st0 + 1, st1 - 1), b1, mr1);
+    store_a(0, a0);
+    store_b(0, b0, mr0);
+    __syncthreads();
+    int st = st0;
+    for (; st + 2 <= st1; st += 2) {
+      step(st, 0, a0, b0, mr0, a1, b1, mr1);
+      step(st + 1, 1, a1, b1, mr1, a0, b0, mr0);
+    }
+    if (st < st1) step(st, 0, a0, b0, mr0, a1, b1, mr1);
+  } else {
   half8_t ar[AIPT];
   u32x4_t br[PB];
   MT mr[PB];
@@ -753,6 +785,7 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
     __syncthreads();
     bc = bn1;
   }
+  }
 
   // epilogue: lane holds rows 4*kq + r of each 16-row block, column n16 of each tile
   if (a.swiglu) {
@@ -774,7 +807,7 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
       for (int i = 0; i < MB; i++) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const int m = m0 + wm * 64 + i * 16 + 4 * kq + r;
+          const int m = m0 + wm * (16 * MB) + i * 16 + 4 * kq + r;
           if (m < mend) {
             const float g = ldexpf(acc[i][2 * pj][r], a.rowexp[m] + ceg);
             const float u = ldexpf(acc[i][2 * pj + 1][r], a.rowexp[m] + ceu);
@@ -792,7 +825,7 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
         float x = rmx[i][r];
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));  // the row's 16 lanes
-        const int m = m0 + wm * 64 + i * 16 + 4 * kq + r;
+        const int m = m0 + wm * (16 * MB) + i * 16 + 4 * kq + r;
         if (n16 == 0 && m < mend) atomicMax(&a.rowmax[m], __float_as_int(x));
       }
     }
@@ -809,7 +842,7 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
       for (int i = 0; i < MB; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const int m = m0 + wm * 64 + i * 16 + 4 * kq + r;
+          const int m = m0 + wm * (16 * MB) + i * 16 + 4 * kq + r;
           if (m < mend) pp[(int64_t)m * a.N + n] = acc[i][j][r];
         }
     }
@@ -825,7 +858,7 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
     for (int i = 0; i < MB; i++) {
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const int m = m0 + wm * 64 + i * 16 + 4 * kq + r;
+        const int m = m0 + wm * (16 * MB) + i * 16 + 4 * kq + r;
         if (m < mend) a.C[(int64_t)m * a.ldc + n] = ldexpf(acc[i][j][r], a.rowexp[m] + ce) + bv;
       }
     }
@@ -849,19 +882,20 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
   C[(int64_t)m * ldc + n] = ldexpf(s, rowexp[m] + ce) + (bias ? bias[n] : 0.f);
 }
 
-template <int KIND, int NP, int BN, int SSX, int WMW, int NBUF>
+template <int KIND, int NP, int BN, int SSX, int WMW, int NBUF, int MB = 4, int RS = 1>
 void launch_lds1(const GemmArgs &a, dim3 grid, hipStream_t st) {
   static bool raised = false;
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
   constexpr int SS = SSX < SPC ? SSX : SPC;
   // LDS: NBUF x (A: NP pieces x SS steps x 4 x rows, B: BN/16 tiles x SS steps x 64) x 16 B
-  constexpr size_t lds = (size_t)NBUF * (NP * SS * 4 * 64 * WMW + (BN / 16) * SS * 64) * 16;
+  constexpr size_t lds =
+      (size_t)NBUF * (NP * SS * 4 * 16 * MB * WMW + (BN / 16) * SS * 64) * 16;
   if constexpr (lds > 160 * 1024) {
     // too big with two A pieces: the same tile with 2-step stages and two buffers (fits)
     static_assert(SSX != 2 || NBUF != 2, "k_gemm_lds tile exceeds the LDS");
-    launch_lds1<KIND, NP, BN, 2, WMW, 2>(a, grid, st);
+    launch_lds1<KIND, NP, BN, 2, WMW, 2, MB, RS>(a, grid, st);
   } else {
-    auto f = k_gemm_lds<KIND, NP, BN, SSX, WMW, NBUF>;
+    auto f = k_gemm_lds<KIND, NP, BN, SSX, WMW, NBUF, MB, RS>;
     if (!raised)
       raised = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
                                    160 * 1024) == hipSuccess;
@@ -869,8 +903,10 @@ void launch_lds1(const GemmArgs &a, dim3 grid, hipStream_t st) {
   }
 }
 
-// tile configurations of k_gemm_lds (rows x columns per workgroup; ring depth 2 or 3); all
-// stages are two MFMA steps
+// tile configurations of k_gemm_lds (rows x columns per workgroup).  All stages are two MFMA
+// steps; each stage's loads are issued two iterations ahead through two register sets (a
+// single set measured 3-5% slower at every M, larger per-wave tiles and 3-buffer rings slower
+// still: the kernel waits on memory and LDS latency with 2 waves per SIMD, not on bandwidth).
 enum { LDS_64x128 = 0, LDS_128x64 = 1, LDS_256x128 = 2 };
 int lds_rows(int cfg) { return cfg == LDS_256x128 ? 256 : cfg == LDS_128x64 ? 128 : 64; }
 int lds_cols(int cfg) { return cfg == LDS_128x64 ? 64 : 128; }
@@ -878,9 +914,9 @@ int lds_cols(int cfg) { return cfg == LDS_128x64 ? 64 : 128; }
 template <int KIND, int NP>
 void launch_lds(const GemmArgs &a, int cfg, dim3 grid, hipStream_t st) {
   switch (cfg) {
-    case LDS_64x128: launch_lds1<KIND, NP, 128, 2, 1, 2>(a, grid, st); break;
-    case LDS_256x128: launch_lds1<KIND, NP, 128, 2, 4, 3>(a, grid, st); break;
-    default: launch_lds1<KIND, NP, 64, 2, 2, 2>(a, grid, st); break;
+    case LDS_64x128: launch_lds1<KIND, NP, 128, 2, 1, 2, 4, 2>(a, grid, st); break;
+    case LDS_256x128: launch_lds1<KIND, NP, 128, 2, 4, 2, 4, 2>(a, grid, st); break;
+    default: launch_lds1<KIND, NP, 64, 2, 2, 2, 4, 2>(a, grid, st); break;
   }
 }
 
