@@ -914,7 +914,8 @@ int lds_cols(int cfg) { return cfg == LDS_128x64 ? 64 : 128; }
 template <int KIND, int NP>
 void launch_lds(const GemmArgs &a, int cfg, dim3 grid, hipStream_t st) {
   switch (cfg) {
-    case LDS_64x128: launch_lds1<KIND, NP, 128, 2, 1, 2, 4, 2>(a, grid, st); break;
+    // 64 x 128 with f32 operands (two A pieces) does not fit two register sets in 256 VGPRs
+    case LDS_64x128: launch_lds1<KIND, NP, 128, 2, 1, 2, 4, NP == 1 ? 2 : 1>(a, grid, st); break;
     case LDS_256x128: launch_lds1<KIND, NP, 128, 2, 4, 2, 4, 2>(a, grid, st); break;
     default: launch_lds1<KIND, NP, 64, 2, 2, 2, 4, 2>(a, grid, st); break;
   }
