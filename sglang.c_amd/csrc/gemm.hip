@@ -738,6 +738,7 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
       compute(p);
       store_a(p ^ 1, as);
       store_b(p ^ 1, bs, ms);
+      __builtin_amdgcn_iglp_opt(1);  // let the scheduler interleave LDS traffic with MFMAs
       __syncthreads();
     };
     load_a(st0, a0);
