@@ -87,7 +87,15 @@ QH_API int sgl_qst_get_raw(sgl_qst *st, const char *name, const char **dtype, in
       shape->count < 1 || shape->count > 4)
     return 0;
   const double s = offs->items[0]->num, t = offs->items[1]->num;
-  if (s < 0 || s > t || t > (double)st->data_len) return 0;
+  if (offs->items[0]->type != QJ_NUM || offs->items[1]->type != QJ_NUM || !(s >= 0) || s > t ||
+      t > (double)st->data_len)
+    return 0;
+  for (int i = 0; i < shape->count; i++) {  /* whole numbers in [0, 2^40]: no later overflow */
+    const qj *d = shape->items[i];
+    if (d->type != QJ_NUM || !(d->num >= 0 && d->num <= 1099511627776.0) ||
+        d->num != (double)(int64_t)d->num)
+      return 0;
+  }
   if (dtype) *dtype = qj_str(e, "dtype", "");
   if (ndim) *ndim = shape->count;
   if (dims) {
@@ -120,7 +128,19 @@ static int raw_get(sgl_qraw_fn fn, void *ctx, const char *name, qraw *r) {
   memset(r, 0, sizeof(*r));
   for (int i = 0; i < 4; i++) r->dims[i] = 1;
   r->dtype = "";
-  if (fn(ctx, name, &r->dtype, &r->ndim, r->dims, &r->bytes, &r->nbytes)) return 1;
+  if (fn(ctx, name, &r->dtype, &r->ndim, r->dims, &r->bytes, &r->nbytes)) {
+    /* a lookup that reports nonsense (dims outside [0, 2^40], 0 or > 4 of them) gets zero
+     * dims, which every shape check below rejects, instead of overflowing their products */
+    int ok = r->ndim >= 1 && r->ndim <= 4 && r->dtype && r->bytes;
+    for (int i = 0; i < 4 && ok; i++) ok = r->dims[i] >= 0 && r->dims[i] <= ((int64_t)1 << 40);
+    if (!ok) {
+      for (int i = 0; i < 4; i++) r->dims[i] = 0;
+      r->ndim = 1;
+      r->nbytes = 0;
+      if (!r->dtype) r->dtype = "";
+    }
+    return 1;
+  }
   memset(r, 0, sizeof(*r));  /* absent: zero dims, as the reference's memset tensors */
   r->dtype = "";
   return 0;

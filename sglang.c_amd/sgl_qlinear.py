@@ -254,7 +254,8 @@ class SafeTensors:
                         C.byref(nb)):
             return None
         data = C.string_at(ptr.value, nb.value) if nb.value else b""
-        return dt.value.decode(), tuple(dims[i] for i in range(nd.value)), data
+        return (dt.value.decode("utf-8", "replace"), tuple(dims[i] for i in range(nd.value)),
+                data)
 
     def probe(self, cfg, base):
         """(rc, info): rc 1 = loadable, 0 = no quantized tensors, -1 = error."""
