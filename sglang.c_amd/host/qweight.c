@@ -22,6 +22,20 @@ QH_API int sgl_q_pack(int bits) { return bits > 0 ? 32 / bits : 0; } /* referenc
 static int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 static int64_t round_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 
+/* Every caller-supplied extent must lie in [0, 2^40) before any shape arithmetic (products of
+ * two of them then stay inside int64).  A weight that large could not be resident anyway. */
+static int extents_ok(const char *what, const int64_t *v, int n) {
+  for (int i = 0; i < n; i++)
+    if (v[i] < 0 || v[i] >= ((int64_t)1 << 40)) {
+      QH_ERR("%s: extent %lld out of range", what, (long long)v[i]);
+      return 0;
+    }
+  return 1;
+}
+#define EXTENTS_OK(what, ...) \
+  extents_ok(what, (const int64_t[]){__VA_ARGS__}, \
+             (int)(sizeof((const int64_t[]){__VA_ARGS__}) / sizeof(int64_t)))
+
 /* Device K positions: groups made contiguous in group order (act-order sorts by g_idx, keeping
  * the original order inside a group), each group padded to a multiple of 32, total padded to a
  * whole number of chunks (spc steps).  kmap[k'] = original k or -1; kinv[k] = k'. */
@@ -149,6 +163,8 @@ static sglq_dev *build_awq_gptq(const sgl_qcfg *cfg, const int32_t *qweight, int
                                 int64_t sc_cols, const int32_t *g_idx, int64_t g_n, int64_t N,
                                 int64_t K, int dev) {
   int64_t ng = 0;
+  if (!EXTENTS_OK("quant", qw_rows, qw_cols, qz_rows, qz_cols, sc_rows, sc_cols, g_n, N, K))
+    return NULL;
   if (check_awq_gptq(cfg, qweight, qw_rows, qw_cols, qzeros, qz_rows, qz_cols, scales, sc_rows,
                      sc_cols, g_idx, g_n, N, K, &ng) != 0)
     return NULL;
@@ -190,6 +206,8 @@ static sglq_dev *build_marlin(const sgl_qcfg *cfg, const int32_t *qweight, int64
                               int64_t qz_cols, const float *scales, int64_t sc_rows,
                               int64_t sc_cols, int64_t N, int64_t K, int dev) {
   if (!cfg || !qweight || !scales || N <= 0 || K <= 0) return NULL;
+  if (!EXTENTS_OK("quant(marlin)", qw_rows, qw_cols, qz_rows, qz_cols, sc_rows, sc_cols, N, K))
+    return NULL;
   const int bits = cfg->bits ? cfg->bits : 4;
   if (bits != 4 && bits != 8) {
     QH_ERR("quant(marlin): 4/8-bit only (config says %d)", bits);
@@ -259,6 +277,7 @@ static sglq_dev *build_ct(const sgl_qcfg *cfg, const int32_t *wpacked, int64_t r
                           const float *scales, int64_t sc_rows, int64_t sc_cols, int64_t N,
                           int64_t K, int dev) {
   if (!cfg || !wpacked || !scales || N <= 0 || K <= 0) return NULL;
+  if (!EXTENTS_OK("quant(ct)", rows, cols, sc_rows, sc_cols, N, K)) return NULL;
   const int bits = cfg->bits ? cfg->bits : 4;
   const int64_t G = cfg->group_size > 0 ? cfg->group_size : K;
   const int off = cfg->offset ? cfg->offset : (1 << (bits - 1));
@@ -309,6 +328,7 @@ static sglq_dev *build_mxfp4(const uint8_t *wpacked, int64_t rows, int64_t cols,
                              const uint8_t *scales, int64_t sc_rows, int64_t sc_cols, int64_t N,
                              int64_t K, int dev) {
   if (!wpacked || !scales || N <= 0 || K <= 0) return NULL;
+  if (!EXTENTS_OK("quant(mxfp4)", rows, cols, sc_rows, sc_cols, N, K)) return NULL;
   if (rows != N) {
     QH_ERR("quant(mxfp4): weight has %lld rows, N=%lld", (long long)rows, (long long)N);
     return NULL;
@@ -350,6 +370,7 @@ static sglq_dev *build_mxfp4(const uint8_t *wpacked, int64_t rows, int64_t cols,
 
 static sglq_dev *build_w8(const int8_t *W, const float *sw, int64_t N, int64_t K, int dev) {
   if (!W || !sw || N <= 0 || K <= 0) return NULL;
+  if (!EXTENTS_OK("w8", N, K)) return NULL;
   sglq_plan p;
   memset(&p, 0, sizeof(p));
   p.src = SGLQ_SRC_W8;

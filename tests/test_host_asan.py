@@ -1,6 +1,9 @@
-"""The host parsers under AddressSanitizer + UBSan: tests/asan/qload_fuzz.c (random header
-mutations through sgl_qst_open / get_raw / sgl_qlinear_probe) built from the product's own
-host sources with gcc and run for a few seeds; any sanitizer report fails the test."""
+"""The host layer under AddressSanitizer + UBSan, built from the product's own host sources
+with gcc and run for a few seeds; any sanitizer report fails the test:
+  tests/asan/qload_fuzz.c    random safetensors header mutations through sgl_qst_open /
+                             get_raw / sgl_qlinear_probe
+  tests/asan/qweight_fuzz.c  random (small, huge, negative) shapes through every
+                             sgl_qlinear_create* / dequant validation, and sgl_qcfg_from_json"""
 import os
 import shutil
 import subprocess
@@ -10,13 +13,20 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def test_qload_parsers_clean_under_asan(tmp_path):
+HOST = os.path.join(ROOT, "sglang.c_amd", "host")
+HARNESSES = {
+    "qload_fuzz.c": ["qload.c", "qjson.c"],
+    "qweight_fuzz.c": ["qweight.c", "qjson.c", "qlog.c", "quant.c"],
+}
+
+
+@pytest.mark.parametrize("harness", sorted(HARNESSES))
+def test_host_layer_clean_under_asan(tmp_path, harness):
     if shutil.which("gcc") is None:
         pytest.skip("gcc not available")
     exe = tmp_path / "fuzz"
-    src = [os.path.join(ROOT, "tests", "asan", "qload_fuzz.c"),
-           os.path.join(ROOT, "sglang.c_amd", "host", "qload.c"),
-           os.path.join(ROOT, "sglang.c_amd", "host", "qjson.c")]
+    src = [os.path.join(ROOT, "tests", "asan", harness)] + \
+        [os.path.join(HOST, f) for f in HARNESSES[harness]]
     cmd = ["gcc", "-std=c11", "-g", "-O1", "-fsanitize=address,undefined",
            "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer",
            "-I" + os.path.join(ROOT, "include"), "-I" + os.path.join(ROOT, "sglang.c_amd", "csrc"),
