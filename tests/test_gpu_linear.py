@@ -84,6 +84,18 @@ def test_prefill_split_over_k(orc, fmt):
     _run(orc, fmt, 1000, 4096, [33, 64, 100, 200], dtypes=("bf16",), bias=True)
 
 
+@pytest.mark.parametrize("fmt", ["gptq4", "mxfp4", "gptq8", "awq4_gemv"])
+def test_prefill_large_tiles(orc, fmt):
+    """256 x 128 tiles (M >= 1024) with ragged M and N, and the M boundaries between the
+    tilings (64 / 65, 1023 / 1024) and between GEMV and GEMM (16 / 17)."""
+    _run(orc, fmt, 1000, 1024, [16, 17, 65, 1023, 1030], dtypes=("bf16",), bias=True)
+
+
+def test_prefill_large_tiles_f32(orc):
+    """f32 activations (two A pieces) through every tiling."""
+    _run(orc, "gptq4", 520, 1024, [40, 300, 1100], dtypes=("f32",))
+
+
 def test_graph_replay_matches_eager(orc):
     """Split-K arrival counters reset themselves: repeated graph replays, with eager work and
     synchronisations between them, all equal the eager result bit for bit."""
