@@ -1,10 +1,10 @@
 // gemm.hip — prefill-side quantized linear, C[M,N] = A[M,K] * W^T (+ bias) for M > 16.
 //
 // Launches:
-//   k_rowexp + k_prep_a  the A operands, once per call: per row an exact power of two that puts
-//             max|a| in [2^13, 2^14), then f16 hi (+ lo for f32 inputs) in the layout
-//             [piece][step][kq][Mpad][8], gathered through kmap (act-order); rows M..Mpad are
-//             zero.
+//   k_prep_rows (or k_rowexp + k_prep_a)  the A operands, once per call: per row an exact
+//             power of two that puts max|a| in [2^13, 2^14), then f16 hi (+ lo for f32 inputs)
+//             in the layout [piece][step][kq][Mpad][8], gathered through kmap (act-order);
+//             rows M..Mpad are zero.
 //   k_gemm_lds  weights whose codes prescale exactly enough into f16 (groups with f16 scales in
 //             [2^-14, 128], and MXFP4): each workgroup unpacks its weight tile once per stage
 //             into LDS next to the A operands, through a ring of LDS buffers, and its waves run
@@ -184,6 +184,100 @@ __global__ __launch_bounds__(256) void k_prep_a(const void *__restrict__ A, int 
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const float x = ldexpf(v[i], -e);
+      const _Float16 h = (_Float16)x;
+      hi[i] = h;
+      lo[i] = (_Float16)(x - (float)h);
+    }
+    aop[(int64_t)it * Mpad + m] = hi;
+    if (split) aop[plane + (int64_t)it * Mpad + m] = lo;
+  }
+}
+
+// k_prep_rows: both steps in one pass for dense or gathered rows (MODE 0/1): 16-byte loads
+// for an identity kmap and 16-byte aligned rows, element gathers through kmap otherwise.  A workgroup owns R whole rows (R divides 256 and Mpad):
+// thread u takes row u % R and items (u + 256 j) / R, holds up to IT items of that row in
+// registers, the row maximum is reduced over the workgroup, and the scaled operands are
+// written from registers, so A is read once and there is no second launch.  Consecutive
+// threads write consecutive rows of one item (R x 16 contiguous bytes).  Bit-identical to
+// k_rowexp + k_prep_a (the maximum is order-independent and the scaling is the same).
+template <int MODE, int IT>
+__global__ __launch_bounds__(256) void k_prep_rows(const void *__restrict__ A, int dt,
+                                                   int64_t lda, int M, int Mpad, int K,
+                                                   int nitems, const int32_t *__restrict__ kmap,
+                                                   const int32_t *__restrict__ rowmap, int R, int xcd, int perm4, int split,
+                                                   half8_t *__restrict__ aop,
+                                                   int *__restrict__ rowexp) {
+  __shared__ float red[4][16];
+  // 16-B items of 8 consecutive rows share a 128-B line: with xcd set (Mpad % 64 == 0, R <= 8)
+  // the 8 / R workgroups of one line run on one XCD (workgroups go round-robin over the 8
+  // XCDs), so that XCD's L2 assembles the line before it is written back
+  int blk = blockIdx.x;
+  if (xcd) {
+    const int G = 8 / R, x = blk & 7, t = blk >> 3;
+    blk = (t / G) * 8 * G + x * G + t % G;
+  }
+  const int u = threadIdx.x, r = u % R, m = blk * R + r;
+  const int64_t src = prep_src<MODE>(rowmap, M, m);
+  const int64_t rb = src * lda;
+  float v[IT][8];
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < IT; j++) {
+    const int it = (u + 256 * j) / R, kb = it * 8;
+    float raw[8];
+    if (kmap) {  // act-order: element i of the item is A[kmap[kb + i]] (-1: padding)
+      int4 k0 = make_int4(-1, -1, -1, -1), k1 = k0;
+      if (src >= 0 && it < nitems) {
+        k0 = *(const int4 *)(kmap + kb);
+        k1 = *(const int4 *)(kmap + kb + 4);
+      }
+      const int kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+      for (int i = 0; i < 8; i++) raw[i] = kk[i] >= 0 ? act_at(A, dt, rb + kk[i]) : 0.f;
+    } else if (src >= 0 && it < nitems && kb + 8 <= K) {
+      if (dt == SGLQ_DT_F32) {
+        const float4 *p = (const float4 *)((const float *)A + rb + kb);
+        const float4 x = p[0], y = p[1];
+        raw[0] = x.x; raw[1] = x.y; raw[2] = x.z; raw[3] = x.w;
+        raw[4] = y.x; raw[5] = y.y; raw[6] = y.z; raw[7] = y.w;
+      } else {
+        const uint4 x = *(const uint4 *)((const uint16_t *)A + rb + kb);
+        const uint32_t wd[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const uint32_t hb = (wd[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+          raw[i] = dt == SGLQ_DT_BF16 ? __uint_as_float(hb << 16)
+                                      : (float)__builtin_bit_cast(_Float16, (uint16_t)hb);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        raw[i] = (src >= 0 && it < nitems && kb + i < K) ? act_at(A, dt, rb + kb + i) : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      v[j][i] = raw[perm4 ? kofs4(i) : i];
+      mx = fmaxf(mx, fabsf(raw[i]));
+    }
+  }
+  // row maximum: lanes u, u ^ o (o >= R) share a row; then the four waves through LDS
+  for (int o = 32; o >= R; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  const int w = u >> 6, lane = u & 63;
+  if (lane < R) red[w][lane] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0][r], red[1][r]), fmaxf(red[2][r], red[3][r]));
+  const int e = row_exponent(mx);
+  if (u < R) rowexp[m] = e;
+  const int64_t plane = (int64_t)nitems * Mpad;
+#pragma unroll
+  for (int j = 0; j < IT; j++) {
+    const int it = (u + 256 * j) / R;
+    if (it >= nitems) continue;
+    half8_t hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float x = ldexpf(v[j][i], -e);
       const _Float16 h = (_Float16)x;
       hi[i] = h;
       lo[i] = (_Float16)(x - (float)h);
@@ -988,6 +1082,39 @@ int sglq_prep_a(const sglq_dev *d, int mode, const void *A, int dt, int64_t lda,
   const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
   const int vec = kmap == nullptr && (uintptr_t)A % 16 == 0 && (lda * esz) % 16 == 0;
   const dim3 pgrid((unsigned)(Mpad / 16), (unsigned)((d->nsteps * 4 + 63) / 64));
+  if (!rowmax && mode != 2 && (vec || kmap) && Mpad % 16 == 0) {
+    // one pass: one row per workgroup (measured fastest at M = 64..2048 against 2..16 rows),
+    // at most 16 items (128 elements) per thread
+    const int64_t nitems = d->nsteps * 4;
+    const int R = 1;
+    const int64_t need = (R * nitems + 255) / 256;
+    if (need <= 16) {
+      const unsigned grid = (unsigned)(Mpad / R);
+      const int xcd = Mpad % 64 == 0 && R <= 8;
+#define SGLQ_PREP_ROWS(MODE, IT)                                                               \
+  k_prep_rows<MODE, IT><<<grid, 256, 0, st>>>(A, dt, lda, (int)M, (int)Mpad, (int)d->K,        \
+                                              (int)nitems, kmap, rowmap, R, xcd, perm4, split, \
+                                              (half8_t *)aop, rowexp)
+#define SGLQ_PREP_ROWS_IT(MODE)         \
+  if (need <= 2)                         \
+    SGLQ_PREP_ROWS(MODE, 2);             \
+  else if (need <= 4)                    \
+    SGLQ_PREP_ROWS(MODE, 4);             \
+  else if (need <= 8)                    \
+    SGLQ_PREP_ROWS(MODE, 8);             \
+  else                                   \
+    SGLQ_PREP_ROWS(MODE, 16)
+      if (mode == 0) {
+        SGLQ_PREP_ROWS_IT(0);
+      } else {
+        SGLQ_PREP_ROWS_IT(1);
+      }
+#undef SGLQ_PREP_ROWS_IT
+#undef SGLQ_PREP_ROWS
+      SGLQ_HIP(hipGetLastError());
+      return 0;
+    }
+  }
 #define SGLQ_PREP(MODE)                                                                       \
   if (!rowmax)                                                                                  \
     k_rowexp<MODE><<<(unsigned)((Mpad + 3) / 4), 256, 0, st>>>(                                 \
@@ -1172,7 +1299,10 @@ int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
               float *C, int64_t ldc, hipStream_t st) {
   const int split = dt == SGLQ_DT_F32;
   const int64_t bmr = sglq_gemm_rows(d, split);
-  const int64_t Mpad = (M + 255) / 256 * 256;  // whole 128- and 256-row blocks
+  // rows of A operands: whole row tiles of the LDS kernel's tiling (it reads no further), else
+  // whole 128- and 256-row blocks
+  const int64_t rt = lds_direct(d) ? lds_rows(lds_plan(d, M).cfg) : 256;
+  const int64_t Mpad = (M + rt - 1) / rt * rt;
   const size_t aop_bytes = sglq_aop_bytes(d, Mpad, split);
   const size_t o_part = (aop_bytes + (size_t)Mpad * sizeof(int) + 255) / 256 * 256;
   const size_t part_bytes =
@@ -1184,6 +1314,6 @@ int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
                                                               : nullptr;
   if (sglq_prep_a(d, 0, A, dt, lda, M, Mpad, nullptr, 0, split, aop, rowexp, st) != 0)
     return -1;
-  return sglq_gemm_run(d, nullptr, aop, rowexp, M, Mpad, Mpad / bmr, split, bias, C, ldc, part,
-                       st);
+  return sglq_gemm_run(d, nullptr, aop, rowexp, M, Mpad, (Mpad + bmr - 1) / bmr, split, bias, C,
+                       ldc, part, st);
 }
