@@ -163,14 +163,20 @@ __device__ __forceinline__ constexpr int kofs4(int i) { return (i >> 1) + 4 * (i
 // step; 2 = f32 activations with at most 8 rows: the lo rows sit right below the hi rows in the
 // staging area (rows M .. 2M-1), so one MFMA covers both and row r + M is added to row r at the
 // end.
-template <int KIND, int CPW, int SPL, bool SCF16, bool STEPM, bool FAST>
+// AM (activations): 0 = staged element by element (act-order gather, unaligned rows, K % 8,
+// SwiGLU rows); 1 = 128-bit loads (FAST) with two items per thread held from before the weight
+// loads; 2 = FAST holding eight (several rows over a long range: items loaded after the
+// weights would only arrive with them, and be loaded twice).
+template <int KIND, int CPW, int SPL, bool SCF16, bool STEPM, int AM>
 __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
+  constexpr bool FAST = AM != 0;
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
   constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
   constexpr bool SPLIT = SPL != 0, FOLD = SPL == 2;
   constexpr int NP = SPL == 1 ? 2 : 1;  // MFMAs per step
   constexpr int RW = SPLIT ? 2 : 1;  // 128-bit words per 8-element activation item
-  constexpr int KEEP = 2;            // items per thread held in registers across the passes
+  constexpr int KEEP = AM == 2 ? 8 : 2;  // items per thread held in registers across the passes
+  constexpr bool KEEPDEC = AM != 2;       // hold them decoded (else raw, decoded twice)
   extern __shared__ half8_t s_act[];  // [NP][M][RS] activation operands, then [waves][64] acc
   __shared__ unsigned s_amax[16];
   __shared__ int s_exp[16];
@@ -258,6 +264,25 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
     for (int o = 0; o < 8; o++) mx = fmaxf(mx, fabsf(v[o]));
     atomicMax(&s_amax[row_of(it)], __float_as_uint(mx));
   };
+  // the same for item it = (first item of the wave) + lane, called by every lane (items past
+  // the end carry zeros): a wave whose items all lie in one row (the usual case: rows hold a
+  // multiple of 64 items) reduces across its lanes first and makes one LDS atomic, not 64 on
+  // one address
+  auto amax_wave = [&](int it, const float (&v)[8]) {
+    const int base = it - lane, last = min(base + 63, items - 1);
+    if (base >= items) return;
+    float mx = 0.f;
+#pragma unroll
+    for (int o = 0; o < 8; o++) mx = fmaxf(mx, fabsf(v[o]));
+    const int ma = row_of(base);
+    if (ma == row_of(last)) {
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      if (lane == 0) atomicMax(&s_amax[ma], __float_as_uint(mx));
+    } else if (it < items) {
+      atomicMax(&s_amax[row_of(it)], __float_as_uint(mx));
+    }
+  };
   auto store_item = [&](int it, const float (&v)[8]) {
     const int m = row_of(it), r = it - m * IPR;
     const int e = s_exp[m];
@@ -315,11 +340,19 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 
   // ---- stage the activations: per-row max |a| -> exact power-of-two scale -> f16 operands
   __syncthreads();  // s_amax cleared
-  float kv[KEEP][8];
+  float kv[KEEPDEC ? KEEP : 1][8];
 #pragma unroll
   for (int j = 0; j < KEEP; j++) {
-    decode_raw(tid + nthr * j, keep[j], kv[j]);
-    if (tid + nthr * j < items) amax_item(tid + nthr * j, kv[j]);
+    float v[8];
+    decode_raw(tid + nthr * j, keep[j], v);
+    if constexpr (AM == 2)
+      amax_wave(tid + nthr * j, v);
+    else if (tid + nthr * j < items)
+      amax_item(tid + nthr * j, v);
+    if constexpr (KEEPDEC) {
+#pragma unroll
+      for (int o = 0; o < 8; o++) kv[j][o] = v[o];
+    }
   }
   for (int it = tid + nthr * KEEP; it < items; it += nthr) {
     Raw x;
@@ -335,8 +368,16 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   }
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < KEEP; j++)
-    if (tid + nthr * j < items) store_item(tid + nthr * j, kv[j]);
+  for (int j = 0; j < KEEP; j++) {
+    if (tid + nthr * j >= items) continue;
+    if constexpr (KEEPDEC) {
+      store_item(tid + nthr * j, kv[KEEPDEC ? j : 0]);
+    } else {
+      float v[8];
+      decode_raw(tid + nthr * j, keep[j], v);
+      store_item(tid + nthr * j, v);
+    }
+  }
   for (int it = tid + nthr * KEEP; it < items; it += nthr) {
     Raw x;
     float v[8];
@@ -501,59 +542,61 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   if (tid == 0) __hip_atomic_store(&a.cnt[cg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int KIND, int CPW, int SPL, bool FAST>
+template <int KIND, int CPW, int SPL, int AM>
 void launch4(const GemvArgs &a, int scf16, int stepm, size_t lds, dim3 grid, unsigned nthr,
              hipStream_t st) {
   if constexpr (KIND == SGLQ_KIND_E2M1) {
-    k_gemv<KIND, CPW, SPL, true, false, FAST><<<grid, nthr, lds, st>>>(a);
+    k_gemv<KIND, CPW, SPL, true, false, AM><<<grid, nthr, lds, st>>>(a);
   } else {
     if (scf16) {
       if (stepm)
-        k_gemv<KIND, CPW, SPL, true, true, FAST><<<grid, nthr, lds, st>>>(a);
+        k_gemv<KIND, CPW, SPL, true, true, AM><<<grid, nthr, lds, st>>>(a);
       else
-        k_gemv<KIND, CPW, SPL, true, false, FAST><<<grid, nthr, lds, st>>>(a);
+        k_gemv<KIND, CPW, SPL, true, false, AM><<<grid, nthr, lds, st>>>(a);
     } else {
       if (stepm)
-        k_gemv<KIND, CPW, SPL, false, true, FAST><<<grid, nthr, lds, st>>>(a);
+        k_gemv<KIND, CPW, SPL, false, true, AM><<<grid, nthr, lds, st>>>(a);
       else
-        k_gemv<KIND, CPW, SPL, false, false, FAST><<<grid, nthr, lds, st>>>(a);
+        k_gemv<KIND, CPW, SPL, false, false, AM><<<grid, nthr, lds, st>>>(a);
     }
   }
 }
 
+template <int KIND, int CPW, int SPL>
+void launch_am(const GemvArgs &a, int scf16, int stepm, int am, size_t lds, dim3 grid,
+               unsigned nthr, hipStream_t st) {
+  if (am == 2)
+    launch4<KIND, CPW, SPL, 2>(a, scf16, stepm, lds, grid, nthr, st);
+  else if (am == 1)
+    launch4<KIND, CPW, SPL, 1>(a, scf16, stepm, lds, grid, nthr, st);
+  else
+    launch4<KIND, CPW, SPL, 0>(a, scf16, stepm, lds, grid, nthr, st);
+}
+
 template <int KIND, int CPW>
-void launch_cpw(const GemvArgs &a, bool split, int scf16, int stepm, bool fast, size_t lds,
+void launch_cpw(const GemvArgs &a, bool split, int scf16, int stepm, int am, size_t lds,
                 dim3 grid, unsigned nthr, hipStream_t st) {
   // f32 activations of at most 8 rows: hi and lo parts share one MFMA
-  if (split && a.M <= 8) {
-    if (fast)
-      launch4<KIND, CPW, 2, true>(a, scf16, stepm, lds, grid, nthr, st);
-    else
-      launch4<KIND, CPW, 2, false>(a, scf16, stepm, lds, grid, nthr, st);
-  } else if (split) {
-    if (fast)
-      launch4<KIND, CPW, 1, true>(a, scf16, stepm, lds, grid, nthr, st);
-    else
-      launch4<KIND, CPW, 1, false>(a, scf16, stepm, lds, grid, nthr, st);
-  } else {
-    if (fast)
-      launch4<KIND, CPW, 0, true>(a, scf16, stepm, lds, grid, nthr, st);
-    else
-      launch4<KIND, CPW, 0, false>(a, scf16, stepm, lds, grid, nthr, st);
-  }
+  if (split && a.M <= 8)
+    launch_am<KIND, CPW, 2>(a, scf16, stepm, am, lds, grid, nthr, st);
+  else if (split)
+    launch_am<KIND, CPW, 1>(a, scf16, stepm, am, lds, grid, nthr, st);
+  else
+    launch_am<KIND, CPW, 0>(a, scf16, stepm, am, lds, grid, nthr, st);
 }
 
 template <int KIND>
-void launch_kind(const GemvArgs &a, int cpw, bool split, int scf16, int stepm, bool fast,
+void launch_kind(const GemvArgs &a, int cpw, bool split, int scf16, int stepm, int am,
                  size_t lds, dim3 grid, unsigned nthr, hipStream_t st) {
   switch (cpw) {
-    case 4: launch_cpw<KIND, 4>(a, split, scf16, stepm, fast, lds, grid, nthr, st); break;
-    case 12: launch_cpw<KIND, 12>(a, split, scf16, stepm, fast, lds, grid, nthr, st); break;
-    default: launch_cpw<KIND, 8>(a, split, scf16, stepm, fast, lds, grid, nthr, st); break;
+    case 4: launch_cpw<KIND, 4>(a, split, scf16, stepm, am, lds, grid, nthr, st); break;
+    case 12: launch_cpw<KIND, 12>(a, split, scf16, stepm, am, lds, grid, nthr, st); break;
+    default: launch_cpw<KIND, 8>(a, split, scf16, stepm, am, lds, grid, nthr, st); break;
   }
 }
 
 constexpr size_t kLdsBudget = 60 * 1024;
+constexpr size_t kLdsBigBudget = 128 * 1024;  // staging of the several-row plan (1 workgroup/CU)
 constexpr int kMaxWaves = 8;  // per workgroup (the kernel's launch bound is 512 threads)
 
 struct Plan {
@@ -585,12 +628,27 @@ Plan plan_gemv(const sglq_dev *d, int64_t M, bool split, bool grouped = false) {
   // short workgroups, each staging a short activation range, beat few long ones even with
   // the partial-sum pass).  One row, or short K, keeps the fewest splits above, and so does
   // the grouped launch (it needs a single K range).
-  if (!grouped && M >= 2 && d->nchunk >= 24) {
+  //
+  // From 8 rows on, every workgroup's staging pass (a max and a conversion per element) is
+  // repeated by each column group, so eight tiles per workgroup (half the column groups) with
+  // the K range cut into at most 8 pieces measured faster, the staging allowed to use up to
+  // 128 KiB (one workgroup per CU): M = 16 [11008, 4096] 22.3 -> 16.5 us (f32), 20.3 -> 15.4
+  // (bf16); [4096, 11008] 30.8 -> 19.1, 21.7 -> 17.7; M = 8 [4096, 11008] 17.3 -> 15.7.  At
+  // 2-4 rows it measured 0.5-1 us slower than four tiles.
+  if (!grouped && M >= 2 && M < 8 && d->nchunk >= 24) {
     for (int cpw : {4, 8, 12}) {
       const int S = (int)((d->nchunk + cpw - 1) / cpw);
       if (cpw > max_chunks) break;
       best = {cpw, 1, 4, S, 0, 0};
       if (S <= 12) break;
+    }
+  } else if (!grouped && M >= 8 && d->nchunk >= 24) {
+    const int64_t big = ((int64_t)kLdsBigBudget / (np * M * 16) - 1) / (d->spc * 4);
+    for (int cpw : {4, 8, 12}) {
+      const int S = (int)((d->nchunk + cpw - 1) / cpw);
+      if (cpw > big) break;
+      best = {cpw, 1, 8, S, 0, 0};
+      if (S <= 8) break;
     }
   }
   // One row over more than 64 chunks (K > 8192 at 4 bits): two slices of 4 chunks on each of
@@ -668,16 +726,19 @@ int launch_gemv(const sglq_dev *d, const GemvArgs &a, const Plan &pl, bool split
                 unsigned gy, hipStream_t st) {
   const dim3 grid((unsigned)(pl.ncg * pl.S), gy);
   const unsigned nthr = (unsigned)(pl.ks * pl.tpg * 64);
+  // activation items per thread beyond the two held by default: hold up to eight
+  const int64_t items = (int64_t)a.M * pl.ks * pl.cpw * d->spc * 4;
+  const int am = !fast ? 0 : items > 2 * (int64_t)nthr ? 2 : 1;
   const int stepm = d->meta_mode == SGLQ_META_STEP;
   switch (d->kind) {
     case SGLQ_KIND_U4:
-      launch_kind<SGLQ_KIND_U4>(a, pl.cpw, split, d->scf16, stepm, fast, pl.lds, grid, nthr, st);
+      launch_kind<SGLQ_KIND_U4>(a, pl.cpw, split, d->scf16, stepm, am, pl.lds, grid, nthr, st);
       break;
     case SGLQ_KIND_U8:
-      launch_kind<SGLQ_KIND_U8>(a, pl.cpw, split, d->scf16, stepm, fast, pl.lds, grid, nthr, st);
+      launch_kind<SGLQ_KIND_U8>(a, pl.cpw, split, d->scf16, stepm, am, pl.lds, grid, nthr, st);
       break;
     default:
-      launch_kind<SGLQ_KIND_E2M1>(a, pl.cpw, split, 1, 0, fast, pl.lds, grid, nthr, st);
+      launch_kind<SGLQ_KIND_E2M1>(a, pl.cpw, split, 1, 0, am, pl.lds, grid, nthr, st);
       break;
   }
   SGLQ_HIP(hipGetLastError());

@@ -96,6 +96,15 @@ def test_prefill_large_tiles_f32(orc):
     _run(orc, "gptq4", 520, 1024, [40, 300, 1100], dtypes=("f32",))
 
 
+@pytest.mark.parametrize("fmt", ["gptq4", "gptq4_act", "gptq8", "mxfp4", "w8", "gptq4_row"])
+def test_gemv_rows_long_k(orc, fmt):
+    """Decode GEMV of 8-16 rows over a long K: eight tiles per workgroup with up to 128 KiB of
+    staging (one workgroup per CU) and eight activation items held per thread; the K range
+    split over workgroups with partial sums; ragged N."""
+    K = 8192 if fmt == "mxfp4" else 11008 if fmt != "gptq4_row" else 11000
+    _run(orc, fmt, 200, K, [8, 12, 16], bias=True)
+
+
 def test_graph_replay_matches_eager(orc):
     """Split-K arrival counters reset themselves: repeated graph replays, with eager work and
     synchronisations between them, all equal the eager result bit for bit."""
