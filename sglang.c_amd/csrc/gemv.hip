@@ -651,6 +651,11 @@ Plan plan_gemv(const sglq_dev *d, int64_t M, bool split, bool grouped = false) {
       if (S <= 8) break;
     }
   }
+  // A short K of 9-16 chunks in one range: 4-chunk slices (more loads in flight per tile than
+  // two 8-chunk slices), two tiles per workgroup from two rows on.  W8 [4864, 896] (14
+  // chunks): M = 1 4.75 -> 4.51 us, M = 8 6.83 -> 5.57 us; every split over K measured slower.
+  if (!grouped && d->nchunk > 8 && d->nchunk <= 16 && 16 <= max_chunks)
+    best = {4, (int)((d->nchunk + 3) / 4), M >= 2 ? 2 : 1, 1, 0, 0};
   // One row over more than 64 chunks (K > 8192 at 4 bits): two slices of 4 chunks on each of
   // two tiles per workgroup and the K range split 8 chunks at a time measured 7% faster than
   // one range of 12-chunk slices ([4096, 11008]: 11.7 vs 12.6 us, weights streamed from HBM).
