@@ -983,10 +983,10 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
 // the scaled fp4 conversion), so the products are bit-identical to k_gemm_lds.  Only the A
 // operands (64 rows, one chunk per stage) go through a double-buffered LDS ring, one chunk
 // ahead in registers.  blockIdx.y selects a slice of the chunks when the call is split over K.
-template <int KIND, int NP, int WN, int D>
+template <int KIND, int NP, int WN, int TN, int D>
 __global__ __launch_bounds__(64 * WN, 2) void k_gemm_breg(GemmArgs a) {
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
-  constexpr int MB = 4, BMR = 64, NT16 = 8, TN = NT16 / WN, NTH = 64 * WN;
+  constexpr int MB = 4, BMR = 64, NT16 = WN * TN, NTH = 64 * WN;
   constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
   constexpr int AITEMS = NP * SPC * 4 * BMR;  // 16-B A items per chunk
   constexpr int AIPT = AITEMS / NTH;
@@ -1200,23 +1200,39 @@ enum { LDS_64x128 = 0, LDS_128x64 = 1, LDS_256x128 = 2 };
 int lds_rows(int cfg) { return cfg == LDS_256x128 ? 256 : cfg == LDS_128x64 ? 128 : 64; }
 int lds_cols(int cfg) { return cfg == LDS_128x64 ? 64 : 128; }
 
-// k_gemm_breg for the grouped (MoE) launches: 4 waves of 2 tiles, codes 2 chunks ahead.  At
-// the DeepSeek shapes (64 experts, 48 rows each on average) it measured 105.7 us (gate/up with
-// the SwiGLU epilogue) and 69.9 us (down, f32 operands), against 123.2 and 114.3 us for
-// k_gemm_lds on the same tile; 2 waves of 4 tiles or 3-4 chunks ahead measured 2-8% slower.
-// Dense calls of at most 64 rows stay on k_gemm_lds (21.7 vs 22.6 us at M = 64 on
-// [11008, 4096], where the split over K leaves each workgroup only 5 chunks).
-template <int KIND, int NP>
-void launch_breg(const GemmArgs &a, dim3 grid, hipStream_t st) {
-  constexpr int WN = 4, D = 2;
+// k_gemm_breg for the grouped (MoE) launches, codes 2 chunks ahead (3-4 chunks measured 2-8%
+// slower).  On k_gemm_lds's 64 x 128 tile it measured 105.7 us (gate/up with the SwiGLU
+// epilogue) and 69.9 us (down, f32 operands) at the DeepSeek shapes, against 123.2 and 114.3
+// us for k_gemm_lds; the wave layouts below improve on that.  Dense calls of at most 64 rows
+// stay on k_gemm_lds (21.7 vs 22.6 us at M = 64 on [11008, 4096], where the split over K
+// leaves each workgroup only 5 chunks).
+template <int KIND, int NP, int WN, int TN>
+void launch_breg1(const GemmArgs &a, dim3 grid, hipStream_t st) {
+  constexpr int D = 2;
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
   constexpr size_t lds = (size_t)2 * NP * SPC * 4 * 64 * 16;
   static bool raised = false;
-  auto f = k_gemm_breg<KIND, NP, WN, D>;
+  auto f = k_gemm_breg<KIND, NP, WN, TN, D>;
   if (!raised)
     raised = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
                                  160 * 1024) == hipSuccess;
   f<<<grid, 64 * WN, lds, st>>>(a);
+}
+// Wave layout of the grouped launches, from a sweep at the DeepSeek shapes (64 experts, 48
+// rows each on average): one A piece (bf16 rows, gate/up with the SwiGLU epilogue) 4 waves of
+// 4 tiles (256 columns: 96.6 us; 4 x 2 103.7, 8 x 2 101.8, 8 x 4 103.8); two pieces (f32 rows,
+// down) 8 waves of 2 tiles (55.8 us; 4 x 2 69.9, 4 x 4 64.0, 8 x 4 59.0).  Wider workgroups
+// re-stage each expert block's A operands for fewer column blocks.
+static void breg_shape(int np, int &wn, int &tn) {
+  wn = np == 1 ? 4 : 8;
+  tn = np == 1 ? 4 : 2;
+}
+template <int KIND, int NP>
+void launch_breg(const GemmArgs &a, dim3 grid, hipStream_t st) {
+  if constexpr (NP == 1)
+    launch_breg1<KIND, NP, 4, 4>(a, grid, st);
+  else
+    launch_breg1<KIND, NP, 8, 2>(a, grid, st);
 }
 
 template <int KIND, int NP>
@@ -1453,7 +1469,9 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
       sglq_log_error("prefill GEMM: no workspace for the split over K");
       return -1;
     }
-    const int cbm = lds_rows(pl.cfg), cbn = lds_cols(pl.cfg);
+    int gwn = 0, gtn = 0;
+    if (grp) breg_shape(split ? 2 : 1, gwn, gtn);
+    const int cbm = grp ? 64 : lds_rows(pl.cfg), cbn = grp ? 16 * gwn * gtn : lds_cols(pl.cfg);
     // grouped: row blocks of one expert each (at most 64 rows); dense: the rows of M
     const int64_t nbm2 = grp ? nblk : (M + cbm - 1) / cbm;
     a.nbn = (int)((d->N + cbn - 1) / cbn);
