@@ -73,6 +73,12 @@ def test_moe_prefill_mxfp4(orc):
     _check(orc, 8, 256, 128, 40, 2, seed=61, fmt="mxfp4")
 
 
+def test_moe_prefill_gptq8_ragged(orc):
+    """8-bit experts (2-step chunks) with an intermediate size of 11 tiles and a hidden size of
+    24 tiles: the last column block of the gate/up pairs and of the down output is partial."""
+    _check(orc, 6, 384, 176, 40, 2, seed=81, fmt="gptq8")
+
+
 def test_moe_prefill_unfused(orc):
     """Group scales below 2^-14 cannot prescale f16 codes: those experts take the register
     unpack GEMM, with SwiGLU formed by its own operand prep."""
