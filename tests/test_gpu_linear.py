@@ -105,6 +105,15 @@ def test_gemv_rows_long_k(orc, fmt):
     _run(orc, fmt, 200, K, [8, 12, 16], bias=True)
 
 
+def test_prefill_prep_fallbacks(orc):
+    """Activation prep paths other than the one-launch row prep: rows whose byte length is not
+    a multiple of 16 (K = 100, 16-bit and f32 activations) and K beyond what one workgroup
+    holds in registers (K = 33024 > 32768), both through the two-launch exponent + operand
+    prep."""
+    _run(orc, "w8", 50, 100, [20, 70])
+    _run(orc, "gptq4", 48, 33024, [17, 70], bias=True)
+
+
 def test_graph_replay_matches_eager(orc):
     """Split-K arrival counters reset themselves: repeated graph replays, with eager work and
     synchronisations between them, all equal the eager result bit for bit."""
