@@ -491,12 +491,13 @@ QH_API sgl_qlinear *sgl_qlinear_create_w8(const int8_t *W, const float *sw, int6
 
 QH_API int sgl_qlinear_forward(sgl_qlinear *ql, const void *A, int a_dtype, int64_t M,
                                const float *bias, float *C, void *stream) {
-  if (!ql || !A || !C || M < 0) return -1;
+  if (!ql || M < 0) return -1;
   if (a_dtype != SGL_QL_F32 && a_dtype != SGL_QL_BF16 && a_dtype != SGL_QL_F16) {
     QH_ERR("qlinear: unknown activation dtype %d", a_dtype);
     return -1;
   }
-  if (M == 0) return 0;
+  if (M == 0) return 0; /* an empty batch: nothing to read or write */
+  if (!A || !C) return -1;
   return sglq_forward(ql->d, A, a_dtype, M, bias, C, stream);
 }
 
@@ -520,9 +521,9 @@ QH_API void sgl_qlinear_destroy(sgl_qlinear *ql) {
 QH_API int sgl_qmoe_forward(sgl_qlinear *const *gate_up, sgl_qlinear *const *down, int n_experts,
                             const void *h, int h_dtype, int64_t T, const int32_t *topk_ids,
                             const float *topk_w, int k, float *out, void *stream) {
-  if (!gate_up || !down || n_experts <= 0 || !h || !topk_ids || !topk_w || !out || T < 0 ||
-      k <= 0)
-    return -1;
+  if (!gate_up || !down || n_experts <= 0 || T < 0 || k <= 0) return -1;
+  if (T == 0) return 0; /* an empty batch: nothing to read or write */
+  if (!h || !topk_ids || !topk_w || !out) return -1;
   sglq_dev **gu = (sglq_dev **)malloc(sizeof(sglq_dev *) * (size_t)n_experts);
   sglq_dev **dn = (sglq_dev **)malloc(sizeof(sglq_dev *) * (size_t)n_experts);
   int rc = -1;
@@ -548,7 +549,9 @@ QH_API int sgl_qmoe_forward(sgl_qlinear *const *gate_up, sgl_qlinear *const *dow
 QH_API int sgl_qmoe_router_logits(const float *router_w, int n_experts, const void *h,
                                   int h_dtype, int64_t T, int64_t E, float *logits,
                                   void *stream) {
-  if (!router_w || !h || !logits || T < 0) return -1;
+  if (T < 0) return -1;
+  if (T == 0) return 0;
+  if (!router_w || !h || !logits) return -1;
   if (h_dtype != SGL_QL_F32 && h_dtype != SGL_QL_BF16 && h_dtype != SGL_QL_F16) {
     QH_ERR("qmoe router: unknown activation dtype %d", h_dtype);
     return -1;
@@ -559,14 +562,18 @@ QH_API int sgl_qmoe_router_logits(const float *router_w, int n_experts, const vo
 QH_API int sgl_qmoe_route(const sgl_qmoe_routing *r, const float *logits, const float *e_bias,
                           int n_experts, int64_t T, int32_t *topk_ids, float *topk_w,
                           void *stream) {
-  if (!r || !logits || !topk_ids || !topk_w || T < 0) return -1;
+  if (!r || T < 0) return -1;
+  if (T == 0) return 0;
+  if (!logits || !topk_ids || !topk_w) return -1;
   return sglq_moe_route(logits, T, n_experts, e_bias, r->sigmoid, r->n_group, r->topk_group,
                         r->k, r->norm_topk, r->routed_scale, topk_ids, topk_w, stream);
 }
 
 QH_API int sgl_qmoe_shared(sgl_qlinear *gate_up, sgl_qlinear *down, const void *h, int h_dtype,
                            int64_t T, float *out, void *stream) {
-  if (!gate_up || !down || !h || !out || T < 0) return -1;
+  if (!gate_up || !down || T < 0) return -1;
+  if (T == 0) return 0;
+  if (!h || !out) return -1;
   if (h_dtype != SGL_QL_F32 && h_dtype != SGL_QL_BF16 && h_dtype != SGL_QL_F16) {
     QH_ERR("qmoe shared: unknown activation dtype %d", h_dtype);
     return -1;
@@ -576,7 +583,9 @@ QH_API int sgl_qmoe_shared(sgl_qlinear *gate_up, sgl_qlinear *down, const void *
 
 QH_API int sgl_qmlp_forward(sgl_qlinear *gate, sgl_qlinear *up, sgl_qlinear *down,
                             const void *h, int h_dtype, int64_t T, float *out, void *stream) {
-  if (!gate || !down || !h || !out || T < 0) return -1;
+  if (!gate || !down || T < 0) return -1;
+  if (T == 0) return 0;
+  if (!h || !out) return -1;
   if (h_dtype != SGL_QL_F32 && h_dtype != SGL_QL_BF16 && h_dtype != SGL_QL_F16) {
     QH_ERR("qmlp: unknown activation dtype %d", h_dtype);
     return -1;
@@ -586,13 +595,17 @@ QH_API int sgl_qmlp_forward(sgl_qlinear *gate, sgl_qlinear *up, sgl_qlinear *dow
 
 QH_API int sgl_quant_rows_i8_dev(const float *x, int8_t *out, float *scales, int64_t rows,
                                  int64_t dim, void *stream) {
-  if (!x || !out || !scales || rows < 0 || dim < 0) return -1;
+  if (rows < 0 || dim < 0) return -1;
+  if (rows == 0 || dim == 0) return 0;
+  if (!x || !out || !scales) return -1;
   return sglq_quant_rows_i8_dev(x, out, scales, rows, dim, stream);
 }
 
 QH_API int sgl_dequant_rows_i8_dev(const int8_t *q, const float *scales, float *out,
                                    int64_t rows, int64_t dim, void *stream) {
-  if (!q || !scales || !out || rows < 0 || dim < 0) return -1;
+  if (rows < 0 || dim < 0) return -1;
+  if (rows == 0 || dim == 0) return 0;
+  if (!q || !scales || !out) return -1;
   return sglq_dequant_rows_i8_dev(q, scales, out, rows, dim, stream);
 }
 

@@ -64,3 +64,37 @@ def test_kv_quant_dev_bit_exact(orc):
     assert np.array_equal(sd.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
     back = q.dequant_rows_i8_dev(qd, sd).cpu().numpy()
     assert np.array_equal(back, q_ref.astype(np.float32) * s_ref[:, None])
+
+
+def test_empty_batches():
+    """Zero rows through every device entry point returns at once, with the empty tensors'
+    NULL data pointers: forward, MoE forward, router logits, routing, shared experts, dense
+    MLP and the int8 row quant/dequant."""
+    import torch
+    import sgl_qlinear as q
+    import synth
+    E, I = 256, 128
+    c, z, s = synth.quantize_groups(synth.normal(3, (2 * I, E), 0.02), 128)
+    qw, qz = synth.gptq_pack(c, z)
+    cfg = q.make_cfg(method=2, bits=4, group_size=128, zero_point=1)
+    gu = q.QLinear.from_awq_gptq(cfg, qw, s, 2 * I, E, qzeros=qz)
+    c, z, s = synth.quantize_groups(synth.normal(4, (E, I), 0.02), 128)
+    qw, qz = synth.gptq_pack(c, z)
+    dn = q.QLinear.from_awq_gptq(cfg, qw, s, E, I, qzeros=qz)
+    h = torch.empty((0, E), device="cuda")
+    print("[gpu] empty batches", flush=True)
+    assert gu.forward(h).shape == (0, 2 * I)
+    ids = torch.empty((0, 2), dtype=torch.int32, device="cuda")
+    wts = torch.empty((0, 2), dtype=torch.float32, device="cuda")
+    assert q.qmoe_forward([gu], [dn], h, ids, wts).shape == (0, E)
+    w = torch.randn(4, E, device="cuda")
+    lg = q.qmoe_router_logits(w, h)
+    assert lg.shape == (0, 4)
+    i2, w2 = q.qmoe_route(lg, 2)
+    assert i2.shape == (0, 2) and w2.shape == (0, 2)
+    out = torch.empty((0, E), device="cuda")
+    q.qmoe_shared(gu, dn, h, out)
+    assert q.qmlp_forward(gu, None, dn, h).shape == (0, E)
+    qq, sc = q.quant_rows_i8_dev(torch.empty((0, E), device="cuda"))
+    assert q.dequant_rows_i8_dev(qq, sc).shape == (0, E)
+    torch.cuda.synchronize()
