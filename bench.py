@@ -32,6 +32,7 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "sglang.c_amd")]
 
 HBM_PEAK_GBS = 8000.0
 F16_PEAK_TFLOPS = 2500.0  # dense bf16/fp16 MFMA (the GEMM runs v_mfma_f32_16x16x32_f16)
+FP4_PEAK_TFLOPS = 10100.0  # dense FP4 MFMA (MXFP4 GEMMs are also reported against it)
 ROTATE_BYTES = 1.1e9
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gptq_gemv_m1_traffic.txt")
 
@@ -158,6 +159,8 @@ def gemm_line(torch, ql, M, K, N, dtype, warmup, tag, out):
     out[tag] = {"TFLOP/s": round(fl / t / 1e12, 2),
                 "frac_f16_mfma_peak": round(fl / t / 1e12 / F16_PEAK_TFLOPS, 4),
                 "us": round(t * 1e6, 1)}
+    if tag.startswith("mxfp4"):  # also against the dense FP4 matrix peak
+        out[tag]["frac_fp4_mfma_peak"] = round(fl / t / 1e12 / FP4_PEAK_TFLOPS, 4)
 
 
 EXTRA_SECTIONS = ("gemv16", "w8", "mxfp4", "gemm", "moe")
