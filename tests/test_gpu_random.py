@@ -1,0 +1,60 @@
+"""Seeded random shapes through sgl_qlinear_forward against the oracle (dequant + the
+reference's f32 matmul, reference src/ops.c:243-279): formats, ragged N and K, every decode
+and prefill plan (M from 1 to 300 crosses the GEMV / GEMM boundary and the GEMM tilings), f32 /
+bf16 / f16 activations, with and without bias.  Tolerance: max|y - y_ref| / max|y_ref| <= 1e-3.
+Each case prints its parameters before it runs, so a failure names it."""
+import numpy as np
+import pytest
+
+import synth
+from linear_cases import build, oracle_forward, oracle_weight, product, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+FMTS = ["gptq4", "gptq4_act", "gptq8", "gptq4_g32", "gptq4_v2", "gptq4_row", "awq4",
+        "awq4_gemv", "awq4_noz", "marlin4_asym", "marlin4_sym", "marlin8_sym", "ct4", "ct8",
+        "ct4_g64", "mxfp4", "w8", "gptq8_g32"]
+MS = [1, 2, 5, 8, 9, 16, 17, 40, 64, 65, 130, 300]
+
+
+def _cases(n, seed=0x5EED0900):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        fmt = FMTS[i % len(FMTS)]
+        N = int(rng.integers(16, 700))
+        K = int(rng.integers(32, 3000))
+        if fmt.startswith("awq") or fmt.startswith("gptq"):  # zeros packed 8 (4) per word
+            N = -(-N // 8) * 8
+        if fmt.startswith("marlin"):
+            N, K = -(-N // 64) * 64, -(-K // 16) * 16
+        M = int(rng.choice(MS))
+        while M * N * K > 2e8 and M > 1:
+            M //= 2
+        dt = ["f32", "bf16", "f16"][int(rng.integers(0, 3))]
+        out.append((fmt, N, K, M, dt, bool(rng.integers(0, 2)), 1000 + i))
+    return out
+
+
+@pytest.mark.parametrize("case", _cases(72), ids=lambda c: "-".join(map(str, c[:5])))
+def test_random_shape(orc, case):
+    import torch
+    fmt, N, K, M, dt, bias, seed = case
+    print(f"[gpu] random case {case}", flush=True)
+    kind, a = build(fmt, N, K, seed=seed)
+    ql = product(kind, a, N, K)
+    W = oracle_weight(orc, kind, a, N, K)
+    A = synth.normal(seed + 1, (M, K))
+    if dt == "bf16":
+        Ab = synth.bf16_bits_to_f32(synth.to_bf16_bits(A))
+        tA = torch.from_numpy(Ab).cuda().to(torch.bfloat16)
+    elif dt == "f16":
+        Ab = A.astype(np.float16).astype(np.float32)
+        tA = torch.from_numpy(Ab).cuda().to(torch.float16)
+    else:
+        Ab = A
+        tA = torch.from_numpy(A).cuda()
+    b = synth.normal(seed + 2, N, 0.1) if bias else None
+    y = ql.forward(tA, bias=None if b is None else torch.from_numpy(b).cuda()).cpu().numpy()
+    e = rel_err(y, oracle_forward(orc, kind, a, W, Ab, b))
+    assert e <= TOL, (case, e)
