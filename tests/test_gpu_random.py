@@ -58,3 +58,28 @@ def test_random_shape(orc, case):
     y = ql.forward(tA, bias=None if b is None else torch.from_numpy(b).cuda()).cpu().numpy()
     e = rel_err(y, oracle_forward(orc, kind, a, W, Ab, b))
     assert e <= TOL, (case, e)
+
+
+def _moe_cases(n, seed=0x5EED0A00):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        fmt = ["gptq4", "mxfp4", "gptq8"][i % 3]
+        n_exp = int(rng.integers(2, 12))
+        E = int(rng.integers(2, 12)) * 64
+        mi = int(rng.integers(2, 20)) * 16
+        T = int(rng.choice([1, 2, 3, 4, 7, 33, 90]))
+        k = int(rng.integers(1, min(n_exp, 4) + 1))
+        dt = ["f32", "bf16"][int(rng.integers(0, 2))]
+        out.append((fmt, n_exp, E, mi, T, k, dt, 2000 + 10 * i))
+    return out
+
+
+@pytest.mark.parametrize("case", _moe_cases(12), ids=lambda c: "-".join(map(str, c[:7])))
+def test_random_moe(orc, case):
+    """Routed-expert FFN (reference src/deepseek.c:655-677) at seeded random sizes: decode
+    (T <= 4, grouped GEMV) and prefill (grouped GEMM) with ragged expert blocks."""
+    from test_gpu_moe import _check
+    fmt, n_exp, E, mi, T, k, dt, seed = case
+    print(f"[gpu] random moe {case}", flush=True)
+    _check(orc, n_exp, E, mi, T, k, seed, dtypes=(dt,), fmt=fmt)
