@@ -83,3 +83,38 @@ def test_random_moe(orc, case):
     fmt, n_exp, E, mi, T, k, dt, seed = case
     print(f"[gpu] random moe {case}", flush=True)
     _check(orc, n_exp, E, mi, T, k, seed, dtypes=(dt,), fmt=fmt)
+
+
+def _route_cases(n, seed=0x5EED0B00):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        ne = int(rng.choice([2, 4, 8, 16, 24, 32, 64, 96, 128, 160, 256]))
+        divs = [g for g in (0, 2, 4, 8) if g == 0 or (ne % g == 0 and ne // g >= 2)]
+        ng = int(rng.choice(divs))
+        tg = int(rng.integers(1, ng + 1)) if ng else 0
+        cap = ne if not ng else tg * (ne // ng)
+        k = int(rng.integers(1, min(cap, 8) + 1))
+        out.append((ne, k, bool(rng.integers(0, 2)), ng, tg, bool(rng.integers(0, 2)),
+                    bool(rng.integers(0, 2)), float(rng.choice([1.0, 2.5])), 3000 + i))
+    return out
+
+
+@pytest.mark.parametrize("case", _route_cases(24), ids=lambda c: "-".join(map(str, c[:7])))
+def test_random_route(orc, case):
+    """Routing (reference src/deepseek.c:593-633) at seeded random expert counts, group
+    limits, top-k, sigmoid / softmax, correction bias, normalisation and scale: ids bit-exact,
+    weights within 2e-6 relative."""
+    import torch
+    import sgl_qlinear as q
+    ne, k, sig, ng, tg, bias, norm, scale, seed = case
+    print(f"[gpu] random route {case}", flush=True)
+    rng = np.random.default_rng(seed)
+    lg = (rng.standard_normal((int(rng.integers(1, 70)), ne)) * 2).astype(np.float32)
+    b = (rng.standard_normal(ne) * 0.1).astype(np.float32) if bias else None
+    ids, w = q.qmoe_route(torch.from_numpy(lg).cuda(), k,
+                          None if b is None else torch.from_numpy(b).cuda(), sig, ng, tg, norm,
+                          scale)
+    rid, rw = orc.moe_route(lg, k, b, sig, ng, tg, norm, scale)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=2e-6, atol=0)
