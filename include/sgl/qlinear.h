@@ -20,7 +20,10 @@
  *
  * All pointers passed to create* are host pointers.  Pointers passed to forward/dequant/moe are
  * device pointers; `stream` is a hipStream_t (NULL = default stream).  A handle is bound to
- * the device it was created on and must not be used by two threads at once.  Functions return
+ * the device it was created on and must not be used by two threads at once, nor by launches on
+ * two streams that can overlap: its operand workspace and split-K arrival counters are per
+ * handle, so such launches race (order them with events, or give each stream its own handle).
+ * Functions return
  * 0 (or a handle) on success and -1 (or NULL) after logging the reason.  A batch of zero rows
  * (M, T or rows = 0) returns 0 at once: its data pointers may be NULL and are not read.
  */
