@@ -148,3 +148,11 @@ def test_deterministic_split_k(orc):
     for M in (16, 64, 256):
         A = torch.from_numpy(synth.normal(24, (M, 11008))).cuda()
         assert torch.equal(ql.forward(A), ql.forward(A)), M
+
+
+@pytest.mark.parametrize("fmt", ["gptq4", "gptq4_act", "mxfp4", "w8", "gptq8"])
+def test_gemv_split_rows(orc, fmt):
+    """17-32 rows (f32) and 17-24 rows (16-bit activations) run as two decode GEMVs, rows 0-15
+    and the rest, on offset A / C; the rows either side of both limits take the GEMM."""
+    _run(orc, fmt, 200, 4096, [17, 20, 24, 25, 32, 33], dtypes=("f32", "bf16", "f16"),
+         bias=True)
