@@ -159,6 +159,171 @@ __device__ __forceinline__ void decode_meta(meta_t<SCF16> m, float &sc, half2_t 
 // element i of a U4 operand holds k-offset {0,4,1,5,2,6,3,7}[i]
 __device__ __forceinline__ constexpr int kofs4(int i) { return (i >> 1) + 4 * (i & 1); }
 
+// Split-K epilogue of a decode GEMV workgroup whose partial sums are stored: the last
+// workgroup of the column group (the last wave of the tile when a.ks > 1, after the other
+// slices' waves have left) adds the partials in K order into C and re-arms the counter.
+__device__ __forceinline__ void gemv_splitk_tail(const GemvArgs &a, int M, int sidx, int cg,
+                                                 int t, bool tvalid, int tid, int lane, int nthr,
+                                                 int &s_last) {
+  // ---- split-K over workgroups: the last workgroup of this column group adds the partials in
+  // K order.  Partials are device-scope stores/loads, so no cache write-back or invalidate is
+  // needed; waiting for the stores' acknowledgement before the arrival increment orders them.
+  // (Only the ks == 0 waves are still running here.)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  // partials of (row r, column nn) added in K order; eight loads are in flight at a time
+  // (one at a time, each waiting for its predecessor, they made the reduction latency-bound)
+  auto sum_parts = [&](int r, int nn) -> float {
+    const float *pp = a.part + (int64_t)r * a.N + nn;
+    const int64_t ss = (int64_t)M * a.N;
+    float sum = 0.f;
+    int s0 = 0;
+    for (; s0 + 8 <= a.S; s0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++)
+        v[q] = __hip_atomic_load(pp + (s0 + q) * ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int q = 0; q < 8; q++) sum += v[q];
+    }
+    for (; s0 < a.S; s0++)
+      sum += __hip_atomic_load(pp + s0 * ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return sum;
+  };
+  if (a.ks > 1) {
+    // the ks != 0 waves have left, so no workgroup barrier is possible: arrivals are counted
+    // per tile, by its ks == 0 wave
+    if (!tvalid) return;
+    int last = 0;
+    if (lane == 0)
+      last = __hip_atomic_fetch_add(&a.cnt[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             a.S - 1;
+    last = __shfl(last, 0);
+    if (!last) return;
+    for (int idx = lane; idx < M * 16; idx += 64) {
+      const int r = idx >> 4, nn = t * 16 + (idx & 15);
+      if (tvalid && nn < a.N)
+        a.C[r * a.ldc + nn] = sum_parts(r, nn) + (a.bias ? a.bias[nn] : 0.f);
+    }
+    if (lane == 0) __hip_atomic_store(&a.cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  __syncthreads();
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(&a.cnt[cg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             a.S - 1;
+  __syncthreads();
+  if (!s_last) return;
+  const int ncol = a.tpg * 16;
+  for (int idx = tid; idx < M * ncol; idx += nthr) {
+    const int r = idx / ncol, nn = cg * ncol + idx % ncol;
+    if (nn < a.N) a.C[r * a.ldc + nn] = sum_parts(r, nn) + (a.bias ? a.bias[nn] : 0.f);
+  }
+  if (tid == 0) __hip_atomic_store(&a.cnt[cg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One wave's weights for CPW chunks of one tile (meta entries, then codes), every address
+// clamped into the weight so the loads are straight-line code issued before any use, and the
+// product of those chunks with the A operands of chunk i, step j at arow_p[(i * SPC + j) * 4]
+// (NP == 2: the lo part at lo_off further).  Chunks past the end (c0 + i >= nchunk) run on a
+// zero scale.
+template <int KIND, int CPW, bool SCF16, bool STEPM>
+struct WaveWeights {
+  static constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
+  static constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
+  static constexpr int NMV = E2M1 ? CPW : (STEPM ? CPW * SPC : CPW);
+  using MT = typename std::conditional<E2M1, uint32_t, meta_t<SCF16>>::type;
+  MT mv[NMV];
+  u32x4_t wv[CPW];
+
+  __device__ __forceinline__ void load(const GemvArgs &a, const u32x4_t *codes, const void *meta,
+                                       int tl, int n16, int lane, int c0) {
+    const int clast = a.nchunk - 1;
+    const int64_t mrow = ((int64_t)tl * 16 + n16) * a.nmeta;
+    if constexpr (E2M1) {
+      const uint32_t *ep = (const uint32_t *)((const uint8_t *)meta + mrow);
+#pragma unroll
+      for (int i = 0; i < CPW; i++) mv[i] = ep[min(c0 + i, clast)];
+    } else if constexpr (STEPM) {
+      const MT *mp = (const MT *)meta + mrow;
+#pragma unroll
+      for (int i = 0; i < CPW * SPC; i++) mv[i] = mp[min(c0 * SPC + i, clast * SPC + SPC - 1)];
+    } else {
+      const MT *mp = (const MT *)meta + mrow;
+      const int cc = min(c0, clast);
+      int g = cc / a.cpg, r = cc - g * a.cpg;
+      const int glast = clast / a.cpg;
+#pragma unroll
+      for (int i = 0; i < CPW; i++) {
+        mv[i] = mp[min(g, glast)];
+        if (++r == a.cpg) {
+          r = 0;
+          g++;
+        }
+      }
+    }
+    const u32x4_t *cp = codes + (int64_t)tl * a.nchunk * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < CPW; i++) wv[i] = __builtin_nontemporal_load(cp + min(c0 + i, clast) * 64);
+  }
+
+  template <int NP>
+  __device__ __forceinline__ float4_t multiply(const GemvArgs &a, const half8_t *arow_p,
+                                               int lo_off, int c0) const {
+    auto read_ops = [&](int i, half8_t (&op)[SPC * NP]) {
+#pragma unroll
+      for (int j = 0; j < SPC; j++) {
+        op[j] = arow_p[(i * SPC + j) * 4];
+        if constexpr (NP == 2) op[SPC + j] = arow_p[lo_off + (i * SPC + j) * 4];
+      }
+    };
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    float4_t pacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    half8_t opc[SPC * NP], opn[SPC * NP];
+    read_ops(0, opc);
+  #pragma unroll
+    for (int i = 0; i < CPW; i++) {
+      const bool live = c0 + i < a.nchunk;
+      if (i + 1 < CPW) read_ops(i + 1, opn);
+      float sc = 0.f;
+      half2_t zA = {0, 0}, zB = {0, 0};
+      if constexpr (!E2M1 && !STEPM) {
+        decode_meta<SCF16>(mv[i], sc, zA, zB);
+        sc = live ? sc : 0.f;
+      }
+  #pragma unroll
+      for (int j = 0; j < SPC; j++) {
+        if constexpr (!E2M1 && STEPM) {
+          decode_meta<SCF16>(mv[i * SPC + j], sc, zA, zB);
+          sc = live ? sc : 0.f;
+        }
+        const half8_t b = unpack<KIND>(wv[i], j, zA, zB);
+        // even and odd chunks accumulate in separate registers: two independent MFMA chains
+        float4_t &tc = pacc[i & 1];
+        tc = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[j], b, tc, 0, 0, 0);
+        if constexpr (NP == 2)
+          tc = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[SPC + j], b, tc, 0, 0, 0);
+        if constexpr (E2M1 || STEPM) {
+          if constexpr (E2M1) {
+            const uint32_t ex = (mv[i] >> (8 * j)) & 255u;
+            sc = (ex == 255u || !live) ? 0.f : ldexpf(1.0f, (int)ex - 127);  // ref qweight.c:361
+          }
+          acc += sc * tc;
+          tc = (float4_t){0.f, 0.f, 0.f, 0.f};
+        }
+      }
+      if constexpr (!E2M1 && !STEPM) {
+        acc += sc * pacc[i & 1];
+        pacc[i & 1] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      }
+  #pragma unroll
+      for (int q = 0; q < SPC * NP; q++) opc[q] = opn[q];
+    }
+    return acc;
+  }
+};
+
 // SPL: 0 = 16-bit activations (one f16 part); 1 = f32 activations as f16 hi + lo, two MFMAs per
 // step; 2 = f32 activations with at most 8 rows: the lo rows sit right below the hi rows in the
 // staging area (rows M .. 2M-1), so one MFMA covers both and row r + M is added to row r at the
@@ -305,37 +470,8 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   // staging so their HBM latency overlaps it.  Chunk indices are clamped into [0, nchunk)
   // (valid memory; chunks past the wave's range are never accumulated), so the loads are
   // straight-line code.
-  const int clast = a.nchunk - 1;
-  constexpr int NMV = E2M1 ? CPW : (STEPM ? CPW * SPC : CPW);
-  using MT = typename std::conditional<E2M1, uint32_t, meta_t<SCF16>>::type;
-  MT mv[NMV];
-  const int64_t mrow = ((int64_t)tl * 16 + n16) * a.nmeta;
-  if constexpr (E2M1) {
-    const uint32_t *ep = (const uint32_t *)((const uint8_t *)meta + mrow);
-#pragma unroll
-    for (int i = 0; i < CPW; i++) mv[i] = ep[min(c0 + i, clast)];
-  } else if constexpr (STEPM) {
-    const MT *mp = (const MT *)meta + mrow;
-#pragma unroll
-    for (int i = 0; i < CPW * SPC; i++) mv[i] = mp[min(c0 * SPC + i, clast * SPC + SPC - 1)];
-  } else {
-    const MT *mp = (const MT *)meta + mrow;
-    const int cc = min(c0, clast);
-    int g = cc / a.cpg, r = cc - g * a.cpg;
-    const int glast = clast / a.cpg;
-#pragma unroll
-    for (int i = 0; i < CPW; i++) {
-      mv[i] = mp[min(g, glast)];
-      if (++r == a.cpg) {
-        r = 0;
-        g++;
-      }
-    }
-  }
-  const u32x4_t *cp = codes + (int64_t)tl * a.nchunk * 64 + lane;
-  u32x4_t wv[CPW];
-#pragma unroll
-  for (int i = 0; i < CPW; i++) wv[i] = __builtin_nontemporal_load(cp + min(c0 + i, clast) * 64);
+  WaveWeights<KIND, CPW, SCF16, STEPM> WW;
+  WW.load(a, codes, meta, tl, n16, lane, c0);
   __builtin_amdgcn_sched_barrier(0);  // keep the whole batch of loads ahead of the staging
 
   // ---- stage the activations: per-row max |a| -> exact power-of-two scale -> f16 operands
@@ -392,55 +528,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   // Lanes of rows >= M read row M-1 instead: an A row only feeds the same row of the
   // product, and rows >= M are never written.
   const half8_t *arow_p = s_act + min(n16, (FOLD ? 2 * M : M) - 1) * RS + ks * CPW * SPC * 4 + kq;
-  auto read_ops = [&](int i, half8_t (&op)[SPC * NP]) {
-#pragma unroll
-    for (int j = 0; j < SPC; j++) {
-      op[j] = arow_p[(i * SPC + j) * 4];
-      if constexpr (NP == 2) op[SPC + j] = arow_p[M * RS + (i * SPC + j) * 4];
-    }
-  };
-  float4_t acc = {0.f, 0.f, 0.f, 0.f};
-  float4_t pacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  half8_t opc[SPC * NP], opn[SPC * NP];
-  read_ops(0, opc);
-#pragma unroll
-  for (int i = 0; i < CPW; i++) {
-    const bool live = c0 + i < a.nchunk;
-    if (i + 1 < CPW) read_ops(i + 1, opn);
-    float sc = 0.f;
-    half2_t zA = {0, 0}, zB = {0, 0};
-    if constexpr (!E2M1 && !STEPM) {
-      decode_meta<SCF16>(mv[i], sc, zA, zB);
-      sc = live ? sc : 0.f;
-    }
-#pragma unroll
-    for (int j = 0; j < SPC; j++) {
-      if constexpr (!E2M1 && STEPM) {
-        decode_meta<SCF16>(mv[i * SPC + j], sc, zA, zB);
-        sc = live ? sc : 0.f;
-      }
-      const half8_t b = unpack<KIND>(wv[i], j, zA, zB);
-      // even and odd chunks accumulate in separate registers: two independent MFMA chains
-      float4_t &tc = pacc[i & 1];
-      tc = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[j], b, tc, 0, 0, 0);
-      if constexpr (NP == 2)
-        tc = __builtin_amdgcn_mfma_f32_16x16x32_f16(opc[SPC + j], b, tc, 0, 0, 0);
-      if constexpr (E2M1 || STEPM) {
-        if constexpr (E2M1) {
-          const uint32_t ex = (mv[i] >> (8 * j)) & 255u;
-          sc = (ex == 255u || !live) ? 0.f : ldexpf(1.0f, (int)ex - 127);  // ref qweight.c:361
-        }
-        acc += sc * tc;
-        tc = (float4_t){0.f, 0.f, 0.f, 0.f};
-      }
-    }
-    if constexpr (!E2M1 && !STEPM) {
-      acc += sc * pacc[i & 1];
-      pacc[i & 1] = (float4_t){0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int q = 0; q < SPC * NP; q++) opc[q] = opn[q];
-  }
+  float4_t acc = WW.template multiply<NP>(a, arow_p, M * RS, c0);
 
   // ---- K slices of one tile are added in slice order through LDS (reusing the staging area)
   if (a.ks > 1) {
@@ -484,62 +572,198 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   }
   if (a.S == 1) return;
 
-  // ---- split-K over workgroups: the last workgroup of this column group adds the partials in
-  // K order.  Partials are device-scope stores/loads, so no cache write-back or invalidate is
-  // needed; waiting for the stores' acknowledgement before the arrival increment orders them.
-  // (Only the ks == 0 waves are still running here.)
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  // partials of (row r, column nn) added in K order; eight loads are in flight at a time
-  // (one at a time, each waiting for its predecessor, they made the reduction latency-bound)
-  auto sum_parts = [&](int r, int nn) -> float {
-    const float *pp = a.part + (int64_t)r * a.N + nn;
-    const int64_t ss = (int64_t)M * a.N;
-    float sum = 0.f;
-    int s0 = 0;
-    for (; s0 + 8 <= a.S; s0 += 8) {
-      float v[8];
+  gemv_splitk_tail(a, M, sidx, cg, t, tvalid, tid, lane, nthr, s_last);
+}
+
+// Decode GEMV of one row with wave-private activation staging: fast activations (identity
+// kmap, 16-byte aligned row), one K slice of CPW chunks per wave (the host launches CPW = 4).  Each wave loads only its own slice of the rows, takes each row's largest |a| over that
+// slice with lane shuffles, and stages the scaled f16 operands in an LDS area of its own, so no
+// workgroup barrier or LDS atomic comes before the multiply.  The power of two belongs to the
+// (wave, row) pair and is undone exactly on the wave's sums, before the slices of a tile are
+// added in slice order; everything after that is as in k_gemv.
+// Measured against k_gemv at M = 1 (graph replay, int4 g128, f32 activations, the same plans):
+// [11008, 4096] 10.2 -> 9.3 us, [4096, 11008] 12.0 -> 10.9 us.  At 2-4 rows it measured slower (the tiles that
+// share a slice each repeat the staging), so it runs one row; the indexing is written for MR rows.
+template <int KIND, int CPW, int SPL, bool SCF16, bool STEPM>
+__global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
+  constexpr int MR = 1;
+  constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
+  constexpr bool FOLD = SPL == 2;                  // f32: hi rows [0, M), lo rows [M, 2M)
+  constexpr int RW = FOLD ? 2 : 1;                 // 128-bit words per 8-element item
+  constexpr int IPR = CPW * SPC * 4;               // items per row of a wave's slice (32..128)
+  constexpr int RS = IPR + 1;                      // LDS row stride (+1 spreads rows over banks)
+  constexpr int LPR = IPR >= 64 ? 64 : IPR;        // lanes of one pass that hold the same row
+  constexpr int QPR = IPR >= 64 ? IPR / 64 : 1;    // passes per row
+  constexpr int NQ = (MR * IPR + 63) / 64;         // passes of 64 items over MR rows
+  extern __shared__ half8_t s_act[];  // [waves][RA][RS] operands, then [waves][64] sums
+  __shared__ int s_e[8][MR];
+  __shared__ int s_last;
+
+  const int nthr = blockDim.x;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int cg = (int)(blockIdx.x % (unsigned)a.ncg), sidx = (int)(blockIdx.x / (unsigned)a.ncg);
+  const int tt = w / a.ks, ks = w - tt * a.ks;
+  const int c0 = (sidx * a.ks + ks) * CPW;  // first chunk of this wave
+  const int M = a.M, RA = FOLD ? 2 * M : M;
+  const int t = cg * a.tpg + tt;
+  const bool tvalid = t < a.ntile;
+  const int tl = min(t, a.ntile - 1);
+  const int n16 = lane & 15, kq = lane >> 4;
+  const int kp0 = c0 * SPC * 32;
+  const int nit = M * IPR;
+
+  // ---- this wave's activation items (item it = 64 q + lane: row it / IPR, 8 elements at
+  // k = kp0 + 8 (it % IPR)), then its weights; all loads issued before any is used
+  u32x4_t raw[NQ][RW];
+  bool ok[NQ];
 #pragma unroll
-      for (int q = 0; q < 8; q++)
-        v[q] = __hip_atomic_load(pp + (s0 + q) * ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int q = 0; q < NQ; q++) {
+    const int it = 64 * q + lane, m = it / IPR, kp = kp0 + (it - m * IPR) * 8;
+    ok[q] = it < nit && kp < a.K;
+    if (64 * q < nit) {  // wave-uniform
+      // element offset in 32 bits (the host keeps the activation block under 2^31 elements)
+      const uint32_t off = (uint32_t)min(m, M - 1) * (uint32_t)a.lda + (ok[q] ? kp : 0);
+      const u32x4_t *p = (const u32x4_t *)((const char *)a.A + off * (FOLD ? 4 : 2));
 #pragma unroll
-      for (int q = 0; q < 8; q++) sum += v[q];
+      for (int i = 0; i < RW; i++) raw[q][i] = p[i];
     }
-    for (; s0 < a.S; s0++)
-      sum += __hip_atomic_load(pp + s0 * ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return sum;
+  }
+  WaveWeights<KIND, CPW, SCF16, STEPM> WW;
+  WW.load(a, a.codes, a.meta, tl, n16, lane, c0);
+  __builtin_amdgcn_sched_barrier(0);  // keep the whole batch of loads ahead of the staging
+
+  auto decode = [&](int q, float (&v)[8]) {
+#pragma unroll
+    for (int o = 0; o < 8; o++) {
+      float x;
+      if constexpr (FOLD)
+        x = __uint_as_float(raw[q][o >> 2][o & 3]);
+      else if (a.adt == SGLQ_DT_BF16)
+        x = bf16_bits((raw[q][0][o >> 1] >> (16 * (o & 1))) & 0xFFFFu);
+      else
+        x = f16_bits((raw[q][0][o >> 1] >> (16 * (o & 1))) & 0xFFFFu);
+      v[o] = ok[q] ? x : 0.f;
+    }
   };
-  if (a.ks > 1) {
-    // the ks != 0 waves have left, so no workgroup barrier is possible: arrivals are counted
-    // per tile, by its ks == 0 wave
-    if (!tvalid) return;
-    int last = 0;
-    if (lane == 0)
-      last = __hip_atomic_fetch_add(&a.cnt[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-             a.S - 1;
-    last = __shfl(last, 0);
-    if (!last) return;
-    for (int idx = lane; idx < M * 16; idx += 64) {
-      const int r = idx >> 4, nn = t * 16 + (idx & 15);
-      if (tvalid && nn < a.N)
-        a.C[r * a.ldc + nn] = sum_parts(r, nn) + (a.bias ? a.bias[nn] : 0.f);
+  // ---- per-row max |a| over the slice: lanes of one row in a pass, then the passes of a row
+  float mq[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; q++) {
+    mq[q] = 0.f;
+    if (64 * q >= nit) continue;
+    float v[8];
+    decode(q, v);
+#pragma unroll
+    for (int o = 0; o < 8; o++) mq[q] = fmaxf(mq[q], fabsf(v[o]));
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) mq[q] = fmaxf(mq[q], __shfl_xor(mq[q], o));
+  }
+  half8_t *base = s_act + w * RA * RS;
+#pragma unroll
+  for (int q = 0; q < NQ; q++) {
+    if (64 * q >= nit) continue;
+    float mx = 0.f;
+#pragma unroll
+    for (int u = 0; u < QPR; u++) mx = fmaxf(mx, mq[q - q % QPR + u]);
+    const int e = (mx > 0.f && mx <= 3.0e38f) ? ilogbf(mx) - 13 : 0;  // max in [2^13, 2^14)
+    const int it = 64 * q + lane, m = it / IPR, r = it - m * IPR;
+    if (it >= nit) continue;
+    if (r == 0) s_e[w][m] = e;
+    float v[8];
+    decode(q, v);
+    half8_t hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float x = ldexpf(v[KIND == SGLQ_KIND_U4 ? kofs4(i) : i], -e);
+      const _Float16 h = (_Float16)x;
+      hi[i] = h;
+      lo[i] = (_Float16)(x - (float)h);
     }
-    if (lane == 0) __hip_atomic_store(&a.cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
+    base[m * RS + r] = hi;
+    if constexpr (FOLD) base[(M + m) * RS + r] = lo;
   }
-  __syncthreads();
-  if (tid == 0)
-    s_last = __hip_atomic_fetch_add(&a.cnt[cg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-             a.S - 1;
-  __syncthreads();
-  if (!s_last) return;
-  const int ncol = a.tpg * 16;
-  for (int idx = tid; idx < M * ncol; idx += nthr) {
-    const int r = idx / ncol, nn = cg * ncol + idx % ncol;
-    if (nn < a.N) a.C[r * a.ldc + nn] = sum_parts(r, nn) + (a.bias ? a.bias[nn] : 0.f);
+  // the staging area and s_e[w] are this wave's own: a wavefront-scope fence orders its LDS
+  // stores before the reads of other lanes of the wave
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // ---- multiply (lanes of rows >= RA read row RA - 1; those product rows are never written)
+  const half8_t *arow_p = base + min(n16, RA - 1) * RS + kq;
+  float4_t acc = WW.template multiply<1>(a, arow_p, 0, c0);
+  if constexpr (FOLD) {
+    // row r (hi part) += row r + M (lo part), as in k_gemv
+    float4_t f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int pr = 4 * kq + i + M, e = (i + M) & 3;
+      const float v = e == 0 ? acc[0] : e == 1 ? acc[1] : e == 2 ? acc[2] : acc[3];
+      f[i] = acc[i] + __shfl(v, ((pr >> 2) & 3) * 16 + n16);
+    }
+    acc = f;
   }
-  if (tid == 0) __hip_atomic_store(&a.cnt[cg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // undo this wave's power of two of row 4 kq + i
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int r = 4 * kq + i;
+    acc[i] = r < M ? ldexpf(acc[i], s_e[w][r < MR ? r : 0]) : 0.f;
+  }
+
+  // ---- K slices of one tile are added in slice order through LDS (reusing the staging area)
+  if (a.ks > 1) {
+    float4_t *red = (float4_t *)s_act;
+    __syncthreads();  // every wave is done reading its operands
+    red[w * 64 + lane] = acc;
+    __syncthreads();
+    if (ks != 0) return;
+    acc = red[w * 64 + lane];
+    for (int q = 1; q < a.ks; q++) acc += red[(w + q) * 64 + lane];
+  }
+  const int n = t * 16 + n16;
+  if (tvalid && n < a.N) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int r = 4 * kq + i;
+      if (r < M) {
+        if (a.S == 1)
+          a.C[(int64_t)r * a.ldc + n] = acc[i] + (a.bias ? a.bias[n] : 0.f);
+        else  // device-scope store: written through to the level all XCDs share
+          __hip_atomic_store(&a.part[((int64_t)sidx * M + r) * a.N + n], acc[i],
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (a.S == 1) return;
+  gemv_splitk_tail(a, M, sidx, cg, t, tvalid, tid, lane, nthr, s_last);
+}
+
+template <int KIND, int CPW, int SPL>
+void launch_wave4(const GemvArgs &a, int scf16, int stepm, size_t lds, dim3 grid,
+                  unsigned nthr, hipStream_t st) {
+  if constexpr (KIND == SGLQ_KIND_E2M1) {
+    k_gemv_wave<KIND, CPW, SPL, true, false><<<grid, nthr, lds, st>>>(a);
+  } else {
+    if (scf16) {
+      if (stepm)
+        k_gemv_wave<KIND, CPW, SPL, true, true><<<grid, nthr, lds, st>>>(a);
+      else
+        k_gemv_wave<KIND, CPW, SPL, true, false><<<grid, nthr, lds, st>>>(a);
+    } else {
+      if (stepm)
+        k_gemv_wave<KIND, CPW, SPL, false, true><<<grid, nthr, lds, st>>>(a);
+      else
+        k_gemv_wave<KIND, CPW, SPL, false, false><<<grid, nthr, lds, st>>>(a);
+    }
+  }
+}
+
+template <int KIND>
+void launch_wave(const GemvArgs &a, bool split, int scf16, int stepm, size_t lds, dim3 grid,
+                 unsigned nthr, hipStream_t st) {
+  if (split)
+    launch_wave4<KIND, 4, 2>(a, scf16, stepm, lds, grid, nthr, st);
+  else
+    launch_wave4<KIND, 4, 0>(a, scf16, stepm, lds, grid, nthr, st);
 }
 
 template <int KIND, int CPW, int SPL, int AM>
@@ -607,7 +831,8 @@ struct Plan {
 // Work split for one launch.  A workgroup stages one K range of the activations in LDS and
 // its ks x tpg waves split that range (ks slices of cpw chunks) over tpg tiles; ranges beyond
 // one workgroup (K longer than the staging budget allows) are added across workgroups.
-Plan plan_gemv(const sglq_dev *d, int64_t M, bool split, bool grouped = false) {
+Plan plan_gemv(const sglq_dev *d, int64_t M, bool split, bool grouped = false,
+               bool wave = false) {
   const int64_t np = split ? 2 : 1;
   const int64_t max_chunks = ((int64_t)kLdsBudget / (np * M * 16) - 1) / (d->spc * 4);
   Plan best = {0, 0, 0, 1 << 30, 0, 0};
@@ -672,6 +897,14 @@ Plan plan_gemv(const sglq_dev *d, int64_t M, bool split, bool grouped = false) {
     else if (nc <= 12 && max_chunks >= 12)
       best = {nc <= 4 ? 4 : nc <= 8 ? 8 : 12, 1, 4, 1, 0, 0};
   }
+  // One row through k_gemv_wave (K over 16 chunks): 4-chunk slices on up to 8 waves of one
+  // tile, the rest of K over workgroups.  Measured best of every (cpw 4/8, ks, tpg) with
+  // ks * tpg <= 8: [11008, 4096] 8.3 us (next (8, 4, 1) 8.8), [4096, 11008] 10.0 us (next
+  // (4, 2, 1) 10.3).
+  if (wave) {
+    const int ks = (int)(d->nchunk < 32 ? (d->nchunk + 3) / 4 : 8);
+    best = {4, ks, 1, (int)((d->nchunk + 4 * ks - 1) / (4 * ks)), 0, 0};
+  }
   best.ncg = (int)((d->ntile + best.tpg - 1) / best.tpg);
   const size_t stage = (size_t)np * M * (best.ks * best.cpw * d->spc * 4 + 1) * 16;
   const size_t red = (size_t)best.ks * best.tpg * 64 * 16;
@@ -727,6 +960,8 @@ GemvArgs base_args(const sglq_dev *d, const Plan &pl, const void *A, int dt, int
   return a;
 }
 
+int stepm_of(const sglq_dev *d) { return d->meta_mode == SGLQ_META_STEP; }
+
 int launch_gemv(const sglq_dev *d, const GemvArgs &a, const Plan &pl, bool split, bool fast,
                 unsigned gy, hipStream_t st) {
   const dim3 grid((unsigned)(pl.ncg * pl.S), gy);
@@ -757,16 +992,42 @@ fail:
 int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
               float *C, int64_t ldc, hipStream_t st) {
   const bool split = dt == SGLQ_DT_F32;
-  const Plan pl = plan_gemv(d, M, split);
   const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
+  const bool fast = d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
+                    (lda * esz) % 16 == 0 && M * lda < (1ll << 31);
+  const bool wave = fast && M == 1 && d->nchunk > 16;
+  const Plan pl = plan_gemv(d, M, split, false, wave);
   if (pl.S > d->gv_split) {
     sglq_log_error("qlinear: GEMV split %d exceeds its state (%d)", pl.S, d->gv_split);
     return -1;
   }
   const GemvArgs a = base_args(d, pl, A, dt, lda, M, bias, C, ldc);
-  const bool fast = d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
-                    (lda * esz) % 16 == 0 && M * lda < (1ll << 31);
+  if (wave) {
+    // wave-private staging: [waves][rows][IPR + 1] operands, or the slice sums
+    const int64_t waves = (int64_t)pl.ks * pl.tpg;
+    const int64_t rows = split ? 2 * M : M;
+    const size_t stage = (size_t)(waves * rows * (pl.cpw * d->spc * 4 + 1) * 16);
+    const size_t red = (size_t)(waves * 64 * 16);
+    const size_t lds = stage > red ? stage : red;
+    const dim3 grid((unsigned)(pl.ncg * pl.S));
+    const unsigned nthr = (unsigned)(waves * 64);
+    switch (d->kind) {
+      case SGLQ_KIND_U4:
+        launch_wave<SGLQ_KIND_U4>(a, split, d->scf16, stepm_of(d), lds, grid, nthr, st);
+        break;
+      case SGLQ_KIND_U8:
+        launch_wave<SGLQ_KIND_U8>(a, split, d->scf16, stepm_of(d), lds, grid, nthr, st);
+        break;
+      default:
+        launch_wave<SGLQ_KIND_E2M1>(a, split, 1, 0, lds, grid, nthr, st);
+        break;
+    }
+    SGLQ_HIP(hipGetLastError());
+    return 0;
+  }
   return launch_gemv(d, a, pl, split, fast, 1, st);
+fail:
+  return -1;
 }
 
 int sglq_gemv_grouped_fits(const sglq_dev *d, int64_t max_rows, int split) {

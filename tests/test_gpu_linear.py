@@ -156,3 +156,13 @@ def test_gemv_split_rows(orc, fmt):
     and the rest, on offset A / C; the rows either side of both limits take the GEMM."""
     _run(orc, fmt, 200, 4096, [17, 20, 24, 25, 32, 33], dtypes=("f32", "bf16", "f16"),
          bias=True)
+
+
+@pytest.mark.parametrize("fmt", ["gptq4", "gptq4_g32", "gptq8", "w8", "mxfp4", "awq4", "ct4_g64",
+                                 "gptq4_noz"])
+def test_gemv_one_row_wave_staging(orc, fmt):
+    """One row over K beyond 16 chunks takes the wave-staged GEMV (each wave stages its own K
+    slice and power of two): K with a partial last chunk (2200), one workgroup range (4096) and
+    ranges added across workgroups (11008); ragged N, bias, every activation dtype."""
+    for K in ([2176, 4096, 8192] if fmt == "mxfp4" else [2200, 4096, 11008]):
+        _run(orc, fmt, 200, K, [1], dtypes=("f32", "bf16", "f16"), bias=True)
