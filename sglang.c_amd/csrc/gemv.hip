@@ -576,20 +576,30 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 }
 
 // Decode GEMV of one row with wave-private activation staging: fast activations (identity
-// kmap, 16-byte aligned row), one K slice of CPW chunks per wave (the host launches CPW = 4).  Each wave loads only its own slice of the rows, takes each row's largest |a| over that
+// kmap, 16-byte aligned row), one K slice of CPW chunks per wave (the host launches CPW = 4).
+// GRP 1 and 2 (MoE decode with one row per segment): blockIdx.y picks the segment, whose
+// expert supplies the weights; the row is A row r (amode 0), A row rowmap[r] (amode 1), or
+// with GRP 2 silu(A[r][k]) * A[r][kcols + k] of an f32 A; C row r is written.  (The segment
+// lookups cost the one-row launches 0.8 us when they were runtime branches, so GRP is a
+// template parameter.)  Each wave loads only its own slice of the rows, takes each row's largest |a| over that
 // slice with lane shuffles, and stages the scaled f16 operands in an LDS area of its own, so no
 // workgroup barrier or LDS atomic comes before the multiply.  The power of two belongs to the
 // (wave, row) pair and is undone exactly on the wave's sums, before the slices of a tile are
 // added in slice order; everything after that is as in k_gemv.
-// Measured against k_gemv at M = 1 (graph replay, int4 g128, f32 activations, the same plans):
-// [11008, 4096] 10.2 -> 9.3 us, [4096, 11008] 12.0 -> 10.9 us.  At 2-4 rows it measured slower (the tiles that
-// share a slice each repeat the staging), so it runs one row; the indexing is written for MR rows.
-template <int KIND, int CPW, int SPL, bool SCF16, bool STEPM>
+// Measured against k_gemv at M = 1 (graph replay, f32 activations): [11008, 4096] 10.2 -> 8.5
+// us, [4096, 11008] 11.6 -> 10.5 us (int4 g128), W8 [4864, 896] 4.6 -> 3.9 us.  At 2-4 rows it
+// measured slower or equal (on four tiles per slice each tile repeats the staging; on one tile
+// per workgroup every workgroup reads the whole block of rows), so it runs one row; the
+// indexing is written for MR rows.
+template <int KIND, int CPW, int SPL, bool SCF16, bool STEPM, int GRP>
 __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
   constexpr int MR = 1;
+  constexpr bool SWI = GRP == 2;
+  static_assert(!SWI || SPL == 2, "SwiGLU rows are f32");
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
   constexpr bool FOLD = SPL == 2;                  // f32: hi rows [0, M), lo rows [M, 2M)
-  constexpr int RW = FOLD ? 2 : 1;                 // 128-bit words per 8-element item
+  constexpr int RW = FOLD ? 2 : 1;                 // 128-bit words per 8-element item (and
+                                                   // as many again for the up half with SWI)
   constexpr int IPR = CPW * SPC * 4;               // items per row of a wave's slice (32..128)
   constexpr int RS = IPR + 1;                      // LDS row stride (+1 spreads rows over banks)
   constexpr int LPR = IPR >= 64 ? 64 : IPR;        // lanes of one pass that hold the same row
@@ -604,7 +614,18 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
   const int cg = (int)(blockIdx.x % (unsigned)a.ncg), sidx = (int)(blockIdx.x / (unsigned)a.ncg);
   const int tt = w / a.ks, ks = w - tt * a.ks;
   const int c0 = (sidx * a.ks + ks) * CPW;  // first chunk of this wave
-  const int M = a.M, RA = FOLD ? 2 * M : M;
+  int M = a.M, row0 = 0;
+  const u32x4_t *codes = a.codes;
+  const void *meta = a.meta;
+  if constexpr (GRP != 0) {
+    if ((int)blockIdx.y >= *a.nseg) return;
+    const int4 sg = a.segs[blockIdx.y];
+    row0 = sg.y;
+    M = sg.z;
+    codes = a.codes_e[sg.x];
+    meta = a.meta_e[sg.x];
+  }
+  const int RA = FOLD ? 2 * M : M;
   const int t = cg * a.tpg + tt;
   const bool tvalid = t < a.ntile;
   const int tl = min(t, a.ntile - 1);
@@ -614,7 +635,7 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
 
   // ---- this wave's activation items (item it = 64 q + lane: row it / IPR, 8 elements at
   // k = kp0 + 8 (it % IPR)), then its weights; all loads issued before any is used
-  u32x4_t raw[NQ][RW];
+  u32x4_t raw[NQ][SWI ? 2 * RW : RW];
   bool ok[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; q++) {
@@ -622,21 +643,31 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
     ok[q] = it < nit && kp < a.K;
     if (64 * q < nit) {  // wave-uniform
       // element offset in 32 bits (the host keeps the activation block under 2^31 elements)
-      const uint32_t off = (uint32_t)min(m, M - 1) * (uint32_t)a.lda + (ok[q] ? kp : 0);
+      const int r = row0 + min(m, M - 1);
+      const uint32_t src = GRP == 1 && a.amode == 1 ? (uint32_t)a.rowmap[r] : (uint32_t)r;
+      const uint32_t off = src * (uint32_t)a.lda + (ok[q] ? kp : 0);
       const u32x4_t *p = (const u32x4_t *)((const char *)a.A + off * (FOLD ? 4 : 2));
 #pragma unroll
       for (int i = 0; i < RW; i++) raw[q][i] = p[i];
+      if constexpr (SWI) {
+        const u32x4_t *pu = (const u32x4_t *)((const float *)a.A + off + a.kcols);
+#pragma unroll
+        for (int i = 0; i < RW; i++) raw[q][RW + i] = pu[i];
+      }
     }
   }
   WaveWeights<KIND, CPW, SCF16, STEPM> WW;
-  WW.load(a, a.codes, a.meta, tl, n16, lane, c0);
+  WW.load(a, codes, meta, tl, n16, lane, c0);
   __builtin_amdgcn_sched_barrier(0);  // keep the whole batch of loads ahead of the staging
 
   auto decode = [&](int q, float (&v)[8]) {
 #pragma unroll
     for (int o = 0; o < 8; o++) {
       float x;
-      if constexpr (FOLD)
+      if constexpr (SWI) {
+        const float g = __uint_as_float(raw[q][o >> 2][o & 3]);  // reference deepseek.c:662-663
+        x = (g / (1.0f + expf(-g))) * __uint_as_float(raw[q][RW + (o >> 2)][o & 3]);
+      } else if constexpr (FOLD)
         x = __uint_as_float(raw[q][o >> 2][o & 3]);
       else if (a.adt == SGLQ_DT_BF16)
         x = bf16_bits((raw[q][0][o >> 1] >> (16 * (o & 1))) & 0xFFFFu);
@@ -726,7 +757,7 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
       const int r = 4 * kq + i;
       if (r < M) {
         if (a.S == 1)
-          a.C[(int64_t)r * a.ldc + n] = acc[i] + (a.bias ? a.bias[n] : 0.f);
+          a.C[(int64_t)(row0 + r) * a.ldc + n] = acc[i] + (a.bias ? a.bias[n] : 0.f);
         else  // device-scope store: written through to the level all XCDs share
           __hip_atomic_store(&a.part[((int64_t)sidx * M + r) * a.N + n], acc[i],
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -737,22 +768,22 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
   gemv_splitk_tail(a, M, sidx, cg, t, tvalid, tid, lane, nthr, s_last);
 }
 
-template <int KIND, int CPW, int SPL>
+template <int KIND, int CPW, int SPL, int GRP>
 void launch_wave4(const GemvArgs &a, int scf16, int stepm, size_t lds, dim3 grid,
                   unsigned nthr, hipStream_t st) {
   if constexpr (KIND == SGLQ_KIND_E2M1) {
-    k_gemv_wave<KIND, CPW, SPL, true, false><<<grid, nthr, lds, st>>>(a);
+    k_gemv_wave<KIND, CPW, SPL, true, false, GRP><<<grid, nthr, lds, st>>>(a);
   } else {
     if (scf16) {
       if (stepm)
-        k_gemv_wave<KIND, CPW, SPL, true, true><<<grid, nthr, lds, st>>>(a);
+        k_gemv_wave<KIND, CPW, SPL, true, true, GRP><<<grid, nthr, lds, st>>>(a);
       else
-        k_gemv_wave<KIND, CPW, SPL, true, false><<<grid, nthr, lds, st>>>(a);
+        k_gemv_wave<KIND, CPW, SPL, true, false, GRP><<<grid, nthr, lds, st>>>(a);
     } else {
       if (stepm)
-        k_gemv_wave<KIND, CPW, SPL, false, true><<<grid, nthr, lds, st>>>(a);
+        k_gemv_wave<KIND, CPW, SPL, false, true, GRP><<<grid, nthr, lds, st>>>(a);
       else
-        k_gemv_wave<KIND, CPW, SPL, false, false><<<grid, nthr, lds, st>>>(a);
+        k_gemv_wave<KIND, CPW, SPL, false, false, GRP><<<grid, nthr, lds, st>>>(a);
     }
   }
 }
@@ -760,10 +791,19 @@ void launch_wave4(const GemvArgs &a, int scf16, int stepm, size_t lds, dim3 grid
 template <int KIND>
 void launch_wave(const GemvArgs &a, bool split, int scf16, int stepm, size_t lds, dim3 grid,
                  unsigned nthr, hipStream_t st) {
-  if (split)
-    launch_wave4<KIND, 4, 2>(a, scf16, stepm, lds, grid, nthr, st);
-  else
-    launch_wave4<KIND, 4, 0>(a, scf16, stepm, lds, grid, nthr, st);
+  if (a.segs == nullptr) {
+    if (split)
+      launch_wave4<KIND, 4, 2, 0>(a, scf16, stepm, lds, grid, nthr, st);
+    else
+      launch_wave4<KIND, 4, 0, 0>(a, scf16, stepm, lds, grid, nthr, st);
+  } else if (a.amode == 2) {
+    launch_wave4<KIND, 4, 2, 2>(a, scf16, stepm, lds, grid, nthr, st);
+  } else {
+    if (split)
+      launch_wave4<KIND, 4, 2, 1>(a, scf16, stepm, lds, grid, nthr, st);
+    else
+      launch_wave4<KIND, 4, 0, 1>(a, scf16, stepm, lds, grid, nthr, st);
+  }
 }
 
 template <int KIND, int CPW, int SPL, int AM>
@@ -897,10 +937,9 @@ Plan plan_gemv(const sglq_dev *d, int64_t M, bool split, bool grouped = false,
     else if (nc <= 12 && max_chunks >= 12)
       best = {nc <= 4 ? 4 : nc <= 8 ? 8 : 12, 1, 4, 1, 0, 0};
   }
-  // One row through k_gemv_wave (K over 16 chunks): 4-chunk slices on up to 8 waves of one
-  // tile, the rest of K over workgroups.  Measured best of every (cpw 4/8, ks, tpg) with
-  // ks * tpg <= 8: [11008, 4096] 8.3 us (next (8, 4, 1) 8.8), [4096, 11008] 10.0 us (next
-  // (4, 2, 1) 10.3).
+  // One row through k_gemv_wave: 4-chunk slices on up to 8 waves of one tile, the rest of K
+  // over workgroups.  Measured best of every (cpw 4/8, ks, tpg) with ks * tpg <= 8:
+  // [11008, 4096] 8.3 us (next (8, 4, 1) 8.8), [4096, 11008] 10.0 us (next (4, 2, 1) 10.3).
   if (wave) {
     const int ks = (int)(d->nchunk < 32 ? (d->nchunk + 3) / 4 : 8);
     best = {4, ks, 1, (int)((d->nchunk + 4 * ks - 1) / (4 * ks)), 0, 0};
@@ -989,45 +1028,53 @@ fail:
 
 }  // namespace
 
+namespace {
+
+// k_gemv_wave over plan pl (one row per launch or per segment), gy segments
+int launch_gemv_wave(const sglq_dev *d, const GemvArgs &a, const Plan &pl, bool split,
+                     unsigned gy, hipStream_t st) {
+  // wave-private staging: [waves][rows][IPR + 1] operands, or the slice sums
+  const int64_t waves = (int64_t)pl.ks * pl.tpg;
+  const int64_t rows = split ? 2 : 1;
+  const size_t stage = (size_t)(waves * rows * (pl.cpw * d->spc * 4 + 1) * 16);
+  const size_t red = (size_t)(waves * 64 * 16);
+  const size_t lds = stage > red ? stage : red;
+  const dim3 grid((unsigned)(pl.ncg * pl.S), gy);
+  const unsigned nthr = (unsigned)(waves * 64);
+  switch (d->kind) {
+    case SGLQ_KIND_U4:
+      launch_wave<SGLQ_KIND_U4>(a, split, d->scf16, stepm_of(d), lds, grid, nthr, st);
+      break;
+    case SGLQ_KIND_U8:
+      launch_wave<SGLQ_KIND_U8>(a, split, d->scf16, stepm_of(d), lds, grid, nthr, st);
+      break;
+    default:
+      launch_wave<SGLQ_KIND_E2M1>(a, split, 1, 0, lds, grid, nthr, st);
+      break;
+  }
+  SGLQ_HIP(hipGetLastError());
+  return 0;
+fail:
+  return -1;
+}
+
+}  // namespace
+
 int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
               float *C, int64_t ldc, hipStream_t st) {
   const bool split = dt == SGLQ_DT_F32;
   const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
   const bool fast = d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
                     (lda * esz) % 16 == 0 && M * lda < (1ll << 31);
-  const bool wave = fast && M == 1 && d->nchunk > 16;
+  const bool wave = fast && M == 1;
   const Plan pl = plan_gemv(d, M, split, false, wave);
   if (pl.S > d->gv_split) {
     sglq_log_error("qlinear: GEMV split %d exceeds its state (%d)", pl.S, d->gv_split);
     return -1;
   }
   const GemvArgs a = base_args(d, pl, A, dt, lda, M, bias, C, ldc);
-  if (wave) {
-    // wave-private staging: [waves][rows][IPR + 1] operands, or the slice sums
-    const int64_t waves = (int64_t)pl.ks * pl.tpg;
-    const int64_t rows = split ? 2 * M : M;
-    const size_t stage = (size_t)(waves * rows * (pl.cpw * d->spc * 4 + 1) * 16);
-    const size_t red = (size_t)(waves * 64 * 16);
-    const size_t lds = stage > red ? stage : red;
-    const dim3 grid((unsigned)(pl.ncg * pl.S));
-    const unsigned nthr = (unsigned)(waves * 64);
-    switch (d->kind) {
-      case SGLQ_KIND_U4:
-        launch_wave<SGLQ_KIND_U4>(a, split, d->scf16, stepm_of(d), lds, grid, nthr, st);
-        break;
-      case SGLQ_KIND_U8:
-        launch_wave<SGLQ_KIND_U8>(a, split, d->scf16, stepm_of(d), lds, grid, nthr, st);
-        break;
-      default:
-        launch_wave<SGLQ_KIND_E2M1>(a, split, 1, 0, lds, grid, nthr, st);
-        break;
-    }
-    SGLQ_HIP(hipGetLastError());
-    return 0;
-  }
+  if (wave) return launch_gemv_wave(d, a, pl, split, 1, st);
   return launch_gemv(d, a, pl, split, fast, 1, st);
-fail:
-  return -1;
 }
 
 int sglq_gemv_grouped_fits(const sglq_dev *d, int64_t max_rows, int split) {
@@ -1054,9 +1101,21 @@ int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows
   a.rowmap = rowmap;
   a.amode = amode;
   a.kcols = kcols;
-  const bool fast = amode != 2 && d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
-                    (lda * esz) % 16 == 0 && a_rows * lda < (1ll << 31);
-  return launch_gemv(d, a, pl, split, fast, (unsigned)max_segs, st);
+  const bool aligned = d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
+                       (lda * esz) % 16 == 0 && a_rows * lda < (1ll << 31);
+  // one row per segment (decode of one token): the wave-staged kernel, SwiGLU rows included
+  // (f32 gate and up halves, both 16-byte aligned), while K fits one workgroup's 8 slices
+  if (max_rows == 1 && aligned && d->nchunk <= 32 &&
+      (amode != 2 || (split && kcols % 4 == 0 && a_rows * lda + kcols < (1ll << 31)))) {
+    const Plan pw = plan_gemv(d, 1, split, false, true);
+    GemvArgs aw = a;
+    aw.S = pw.S;
+    aw.ncg = pw.ncg;
+    aw.ks = pw.ks;
+    aw.tpg = pw.tpg;
+    return launch_gemv_wave(d, aw, pw, split, (unsigned)max_segs, st);
+  }
+  return launch_gemv(d, a, pl, split, amode != 2 && aligned, (unsigned)max_segs, st);
 }
 
 extern "C" int sglq_forward(sglq_dev *d, const void *A, int dt, int64_t M, const float *bias,

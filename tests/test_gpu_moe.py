@@ -98,3 +98,12 @@ def test_moe_decode_deepseek_shape(orc):
 def test_moe_prefill_deepseek_shape(orc):
     """BASELINE config 5, prefill: 512 tokens, top-6 of 64 experts, hidden 2048, inter 1408."""
     _check(orc, 64, 2048, 1408, 512, 6, seed=0x5EED0005, dtypes=("bf16",))
+
+
+@pytest.mark.parametrize("fmt", ["gptq4", "mxfp4", "gptq8"])
+def test_moe_decode_one_token(orc, fmt):
+    """One token: one row per expert segment, so both grouped launches take the wave-staged
+    GEMV (token rows gathered for gate/up; SwiGLU rows formed while loading for down), with
+    and without unrouted slots."""
+    _check(orc, 8, 512, 256, 1, 3, seed=91, fmt=fmt)
+    _check(orc, 6, 256, 384, 1, 4, seed=93, fmt=fmt, dtypes=("f32",), drop=True)
