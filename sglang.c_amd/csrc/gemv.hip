@@ -46,6 +46,12 @@ struct GemvArgs {
   const int32_t *rowmap;
   int amode, kcols;
   uint32_t ipr_magic;  // ceil(2^32 / items per row)
+  // one-token MoE down projection with the combine fused (k_gemv_wave GRP 2): the last segment
+  // of a tile to finish writes cout[n] = sum over slots j of cw[j] * C[cpos[j]][n], in slot order
+  const int32_t *cpos;
+  const float *cw;
+  float *cout;
+  int ck;
 };
 
 __device__ __forceinline__ float bf16_bits(uint32_t b) { return __uint_as_float(b << 16); }
@@ -618,7 +624,14 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
   const u32x4_t *codes = a.codes;
   const void *meta = a.meta;
   if constexpr (GRP != 0) {
-    if ((int)blockIdx.y >= *a.nseg) return;
+    const int ns = *a.nseg;
+    if (GRP == 2 && a.cout && ns == 0) {
+      // no routed slot: the combined row is zero
+      const int n = (cg * a.tpg) * 16 + lane;
+      if (blockIdx.y == 0 && w == 0 && lane < 16 && n < a.N) a.cout[n] = 0.f;
+      return;
+    }
+    if ((int)blockIdx.y >= ns) return;
     const int4 sg = a.segs[blockIdx.y];
     row0 = sg.y;
     M = sg.z;
@@ -756,12 +769,46 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
     for (int i = 0; i < 4; i++) {
       const int r = 4 * kq + i;
       if (r < M) {
-        if (a.S == 1)
-          a.C[(int64_t)(row0 + r) * a.ldc + n] = acc[i] + (a.bias ? a.bias[n] : 0.f);
+        float *dst = &a.C[(int64_t)(row0 + r) * a.ldc + n];
+        if (GRP == 2 && a.cout)  // read back by another workgroup's combine
+          __hip_atomic_store(dst, acc[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else if (a.S == 1)
+          *dst = acc[i] + (a.bias ? a.bias[n] : 0.f);
         else  // device-scope store: written through to the level all XCDs share
           __hip_atomic_store(&a.part[((int64_t)sidx * M + r) * a.N + n], acc[i],
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
+    }
+  }
+  if constexpr (GRP == 2) {
+    if (a.cout) {
+      // fused combine (one K range, one live wave per workgroup here): the stores above are
+      // acknowledged before the arrival, and the last segment of the tile reads them back
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      if (!tvalid) return;
+      int last = 0;
+      if (lane == 0)
+        last = __hip_atomic_fetch_add(&a.cnt[t], 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == *a.nseg - 1;
+      last = __shfl(last, 0);
+      if (!last) return;
+      if (lane < 16 && n < a.N) {
+        // ((0 + w0 o0) + w1 o1) + ... in slot order, as k_moe_combine (reference
+        // src/deepseek.c:675-676)
+        float sum = 0.f;
+        for (int j = 0; j < a.ck; j++) {
+          const int r = a.cpos[j];
+          if (r < 0) continue;
+          const float v = __hip_atomic_load(&a.C[(int64_t)r * a.ldc + n], __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+          sum = __fadd_rn(sum, __fmul_rn(a.cw[j], v));
+        }
+        a.cout[n] = sum;
+      }
+      if (lane == 0) __hip_atomic_store(&a.cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
     }
   }
   if (a.S == 1) return;
@@ -1084,7 +1131,7 @@ int sglq_gemv_grouped_fits(const sglq_dev *d, int64_t max_rows, int split) {
 int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows,
                       int64_t max_segs, const void *A, int dt, int64_t a_rows, int64_t lda,
                       int amode, const int32_t *rowmap, int kcols, float *C, int64_t ldc,
-                      hipStream_t st) {
+                      hipStream_t st, const sglq_combine *cmb) {
   const bool split = dt == SGLQ_DT_F32;
   const Plan pl = plan_gemv(d, max_rows, split, true);
   const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
@@ -1113,6 +1160,14 @@ int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows
     aw.ncg = pw.ncg;
     aw.ks = pw.ks;
     aw.tpg = pw.tpg;
+    // the combine needs an arrival counter per tile (allocated with the split-K state)
+    if (cmb && amode == 2 && d->gv_cnt && pw.S == 1) {
+      aw.cpos = cmb->pos;
+      aw.cw = cmb->wts;
+      aw.cout = cmb->out;
+      aw.ck = cmb->k;
+      *cmb->done = 1;
+    }
     return launch_gemv_wave(d, aw, pw, split, (unsigned)max_segs, st);
   }
   return launch_gemv(d, a, pl, split, amode != 2 && aligned, (unsigned)max_segs, st);

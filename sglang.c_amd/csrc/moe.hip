@@ -214,13 +214,16 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
                      segs, nseg};
     // decode-sized batches (every expert has at most T <= 4 rows): grouped GEMVs that read the
     // token rows and the SwiGLU rows directly; otherwise operand prep + grouped GEMMs
+    int combined = 0;
     if (decode) {
       const int64_t max_segs = P < n_exp ? P : n_exp;
       if (sglq_gemv_grouped(g0, &g1, T, max_segs, h, h_dtype, T, E, 1, rowmap, 0, gu, 2 * mi,
                             st) != 0)
         return -1;
+      // one token: the down launch also does the combine when it can
+      const sglq_combine cb = {pos, topk_w, k, out, &combined};
       if (sglq_gemv_grouped(d0, &g2, T, max_segs, gu, SGLQ_DT_F32, P, 2 * mi, 2, nullptr,
-                            (int)mi, o, E, st) != 0)
+                            (int)mi, o, E, st, T == 1 ? &cb : nullptr) != 0)
         return -1;
     } else if (fuse) {
       // act[r] = silu(gate) * up of row r, [P, mi] f32, written by the gate/up GEMM together
@@ -254,9 +257,11 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
                         nullptr, o, E, nullptr, st) != 0)
         return -1;
     }
-    dim3 grid((unsigned)((E + 255) / 256), (unsigned)T);
-    k_moe_combine<<<grid, 256, 0, st>>>(o, E, pos, topk_w, k, (int)E, out);
-    SGLQ_HIP(hipGetLastError());
+    if (!combined) {
+      dim3 grid((unsigned)((E + 255) / 256), (unsigned)T);
+      k_moe_combine<<<grid, 256, 0, st>>>(o, E, pos, topk_w, k, (int)E, out);
+      SGLQ_HIP(hipGetLastError());
+    }
   }
   return 0;
 fail:

@@ -126,10 +126,19 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop, con
 // rowmap[r], 2 silu(A[r][k]) * A[r][kcols + k] with f32 A; A has a_rows rows).  Only when every workgroup can take
 // all of K (sglq_gemv_grouped_fits).
 int sglq_gemv_grouped_fits(const sglq_dev *d, int64_t max_rows, int split);
+// cmb (optional, one token): the down launch also forms out[n] = sum_j wts[j] * C[pos[j]][n]
+// in slot order when its kernel can (then *cmb->done is set to 1, else left alone).
+struct sglq_combine {
+  const int32_t *pos;
+  const float *wts;
+  int k;
+  float *out;
+  int *done;
+};
 int sglq_gemv_grouped(const sglq_dev *d, const struct sglq_group *grp, int64_t max_rows,
                       int64_t max_segs, const void *A, int dt, int64_t a_rows, int64_t lda,
                       int amode, const int32_t *rowmap, int kcols, float *C, int64_t ldc,
-                      hipStream_t st);
+                      hipStream_t st, const sglq_combine *cmb = nullptr);
 // Picks the decode GEMV split for a freshly built weight and allocates its state.
 int sglq_gemv_setup(sglq_dev *d);
 

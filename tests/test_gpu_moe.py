@@ -40,7 +40,9 @@ def _check(orc, n_exp, E, mi, T, k, seed, dtypes=("bf16", "f32"), drop=False, fm
     import sgl_qlinear as q
     gu, dn, wgu, wdn = _experts(orc, n_exp, E, mi, seed, fmt, std)
     ids, wts = synth.moe_routing(seed + 999, T, n_exp, k)
-    if drop:  # unrouted slots (id -1) are skipped
+    if drop == "all":  # no routed slot at all: the output is zero
+        ids[:] = -1
+    elif drop:  # unrouted slots (id -1) are skipped
         ids[::3, -1] = -1
     h = synth.normal(seed + 1000, (T, E))
     for dt in dtypes:
@@ -103,7 +105,9 @@ def test_moe_prefill_deepseek_shape(orc):
 @pytest.mark.parametrize("fmt", ["gptq4", "mxfp4", "gptq8"])
 def test_moe_decode_one_token(orc, fmt):
     """One token: one row per expert segment, so both grouped launches take the wave-staged
-    GEMV (token rows gathered for gate/up; SwiGLU rows formed while loading for down), with
-    and without unrouted slots."""
+    GEMV (token rows gathered for gate/up; SwiGLU rows formed while loading for down, and the
+    weighted combine done by the last segment of each tile), with and without unrouted slots,
+    and with none routed at all (zero output)."""
     _check(orc, 8, 512, 256, 1, 3, seed=91, fmt=fmt)
     _check(orc, 6, 256, 384, 1, 4, seed=93, fmt=fmt, dtypes=("f32",), drop=True)
+    _check(orc, 4, 256, 128, 1, 2, seed=95, fmt=fmt, dtypes=("bf16",), drop="all")
