@@ -581,8 +581,9 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
   gemv_splitk_tail(a, M, sidx, cg, t, tvalid, tid, lane, nthr, s_last);
 }
 
-// Decode GEMV of one row with wave-private activation staging: fast activations (identity
-// kmap, 16-byte aligned row), one K slice of CPW chunks per wave (the host launches CPW = 4).
+// Decode GEMV of one row (or MR = 2 rows) with wave-private activation staging: fast
+// activations (identity kmap, 16-byte aligned rows), one K slice of CPW chunks per wave (the
+// host launches CPW = 4).
 // GRP 1 and 2 (MoE decode with one row per segment): blockIdx.y picks the segment, whose
 // expert supplies the weights; the row is A row r (amode 0), A row rowmap[r] (amode 1), or
 // with GRP 2 silu(A[r][k]) * A[r][kcols + k] of an f32 A; C row r is written.  (The segment
@@ -595,11 +596,11 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 // Measured against k_gemv at M = 1 (graph replay, f32 activations): [11008, 4096] 10.2 -> 8.5
 // us, [4096, 11008] 11.6 -> 10.5 us (int4 g128), W8 [4864, 896] 4.6 -> 3.9 us.  At 2-4 rows it
 // measured slower or equal (on four tiles per slice each tile repeats the staging; on one tile
-// per workgroup every workgroup reads the whole block of rows), so it runs one row; the
-// indexing is written for MR rows.
-template <int KIND, int CPW, int SPL, bool SCF16, bool STEPM, int GRP>
+// per workgroup every workgroup reads the whole block of rows), so it runs one row, or two
+// rows over K of 17-32 chunks (one workgroup range), where it measured faster.
+template <int KIND, int CPW, int SPL, bool SCF16, bool STEPM, int GRP, int MR>
 __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
-  constexpr int MR = 1;
+  static_assert(MR == 1 || GRP == 0, "grouped launches stage one row");
   constexpr bool SWI = GRP == 2;
   static_assert(!SWI || SPL == 2, "SwiGLU rows are f32");
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
@@ -815,22 +816,22 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
   gemv_splitk_tail(a, M, sidx, cg, t, tvalid, tid, lane, nthr, s_last);
 }
 
-template <int KIND, int CPW, int SPL, int GRP>
+template <int KIND, int CPW, int SPL, int GRP, int MR = 1>
 void launch_wave4(const GemvArgs &a, int scf16, int stepm, size_t lds, dim3 grid,
                   unsigned nthr, hipStream_t st) {
   if constexpr (KIND == SGLQ_KIND_E2M1) {
-    k_gemv_wave<KIND, CPW, SPL, true, false, GRP><<<grid, nthr, lds, st>>>(a);
+    k_gemv_wave<KIND, CPW, SPL, true, false, GRP, MR><<<grid, nthr, lds, st>>>(a);
   } else {
     if (scf16) {
       if (stepm)
-        k_gemv_wave<KIND, CPW, SPL, true, true, GRP><<<grid, nthr, lds, st>>>(a);
+        k_gemv_wave<KIND, CPW, SPL, true, true, GRP, MR><<<grid, nthr, lds, st>>>(a);
       else
-        k_gemv_wave<KIND, CPW, SPL, true, false, GRP><<<grid, nthr, lds, st>>>(a);
+        k_gemv_wave<KIND, CPW, SPL, true, false, GRP, MR><<<grid, nthr, lds, st>>>(a);
     } else {
       if (stepm)
-        k_gemv_wave<KIND, CPW, SPL, false, true, GRP><<<grid, nthr, lds, st>>>(a);
+        k_gemv_wave<KIND, CPW, SPL, false, true, GRP, MR><<<grid, nthr, lds, st>>>(a);
       else
-        k_gemv_wave<KIND, CPW, SPL, false, false, GRP><<<grid, nthr, lds, st>>>(a);
+        k_gemv_wave<KIND, CPW, SPL, false, false, GRP, MR><<<grid, nthr, lds, st>>>(a);
     }
   }
 }
@@ -838,7 +839,12 @@ void launch_wave4(const GemvArgs &a, int scf16, int stepm, size_t lds, dim3 grid
 template <int KIND>
 void launch_wave(const GemvArgs &a, bool split, int scf16, int stepm, size_t lds, dim3 grid,
                  unsigned nthr, hipStream_t st) {
-  if (a.segs == nullptr) {
+  if (a.segs == nullptr && a.M == 2) {
+    if (split)
+      launch_wave4<KIND, 4, 2, 0, 2>(a, scf16, stepm, lds, grid, nthr, st);
+    else
+      launch_wave4<KIND, 4, 0, 0, 2>(a, scf16, stepm, lds, grid, nthr, st);
+  } else if (a.segs == nullptr) {
     if (split)
       launch_wave4<KIND, 4, 2, 0>(a, scf16, stepm, lds, grid, nthr, st);
     else
@@ -1082,7 +1088,7 @@ int launch_gemv_wave(const sglq_dev *d, const GemvArgs &a, const Plan &pl, bool 
                      unsigned gy, hipStream_t st) {
   // wave-private staging: [waves][rows][IPR + 1] operands, or the slice sums
   const int64_t waves = (int64_t)pl.ks * pl.tpg;
-  const int64_t rows = split ? 2 : 1;
+  const int64_t rows = (split ? 2 : 1) * a.M;  // a.M = 1 for grouped launches
   const size_t stage = (size_t)(waves * rows * (pl.cpw * d->spc * 4 + 1) * 16);
   const size_t red = (size_t)(waves * 64 * 16);
   const size_t lds = stage > red ? stage : red;
@@ -1113,7 +1119,9 @@ int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
   const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
   const bool fast = d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
                     (lda * esz) % 16 == 0 && M * lda < (1ll << 31);
-  const bool wave = fast && M == 1;
+  // two rows only while K fits one workgroup range: [11008, 4096] 11.2 -> 9.8 us (f32), 10.2 ->
+  // 9.7 (bf16); with K split over workgroups ([4096, 11008]) it measured equal or slower
+  const bool wave = fast && (M == 1 || (M == 2 && d->nchunk > 16 && d->nchunk <= 32));
   const Plan pl = plan_gemv(d, M, split, false, wave);
   if (pl.S > d->gv_split) {
     sglq_log_error("qlinear: GEMV split %d exceeds its state (%d)", pl.S, d->gv_split);

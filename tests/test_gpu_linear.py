@@ -166,3 +166,11 @@ def test_gemv_one_row_wave_staging(orc, fmt):
     ranges added across workgroups (11008); ragged N, bias, every activation dtype."""
     for K in ([2176, 4096, 8192] if fmt == "mxfp4" else [2200, 4096, 11008]):
         _run(orc, fmt, 200, K, [1], dtypes=("f32", "bf16", "f16"), bias=True)
+
+
+@pytest.mark.parametrize("fmt", ["gptq4", "gptq8", "w8", "mxfp4", "gptq4_g32"])
+def test_gemv_two_rows_wave_staging(orc, fmt):
+    """Two rows over K of 17-32 chunks take the two-row wave-staged GEMV (one workgroup
+    range; a partial last chunk at K = 2200); three rows and a longer K stay on k_gemv."""
+    for K in ([2176, 4096] if fmt == "mxfp4" else [2200, 4096, 5000]):
+        _run(orc, fmt, 200, K, [2, 3], dtypes=("f32", "bf16", "f16"), bias=True)
