@@ -583,7 +583,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 
 // Decode GEMV of one row (or MR = 2 rows) with wave-private activation staging: fast
 // activations (identity kmap, 16-byte aligned rows), one K slice of CPW chunks per wave (the
-// host launches CPW = 4).
+// host launches CPW = 4, and 12 for one row over 65-96 chunks).
 // GRP 1 and 2 (MoE decode with one row per segment): blockIdx.y picks the segment, whose
 // expert supplies the weights; the row is A row r (amode 0), A row rowmap[r] (amode 1), or
 // with GRP 2 silu(A[r][k]) * A[r][kcols + k] of an f32 A; C row r is written.  (The segment
@@ -837,13 +837,18 @@ void launch_wave4(const GemvArgs &a, int scf16, int stepm, size_t lds, dim3 grid
 }
 
 template <int KIND>
-void launch_wave(const GemvArgs &a, bool split, int scf16, int stepm, size_t lds, dim3 grid,
-                 unsigned nthr, hipStream_t st) {
+void launch_wave(const GemvArgs &a, int cpw, bool split, int scf16, int stepm, size_t lds,
+                 dim3 grid, unsigned nthr, hipStream_t st) {
   if (a.segs == nullptr && a.M == 2) {
     if (split)
       launch_wave4<KIND, 4, 2, 0, 2>(a, scf16, stepm, lds, grid, nthr, st);
     else
       launch_wave4<KIND, 4, 0, 0, 2>(a, scf16, stepm, lds, grid, nthr, st);
+  } else if (a.segs == nullptr && cpw == 12) {
+    if (split)
+      launch_wave4<KIND, 12, 2, 0>(a, scf16, stepm, lds, grid, nthr, st);
+    else
+      launch_wave4<KIND, 12, 0, 0>(a, scf16, stepm, lds, grid, nthr, st);
   } else if (a.segs == nullptr) {
     if (split)
       launch_wave4<KIND, 4, 2, 0>(a, scf16, stepm, lds, grid, nthr, st);
@@ -993,9 +998,13 @@ Plan plan_gemv(const sglq_dev *d, int64_t M, bool split, bool grouped = false,
   // One row through k_gemv_wave: 4-chunk slices on up to 8 waves of one tile, the rest of K
   // over workgroups.  Measured best of every (cpw 4/8, ks, tpg) with ks * tpg <= 8:
   // [11008, 4096] 8.3 us (next (8, 4, 1) 8.8), [4096, 11008] 10.0 us (next (4, 2, 1) 10.3).
+  // Over 64-96 chunks one row takes 12-chunk slices, all of K in one workgroup (no partial
+  // sums): [4096, 11008] 10.4 -> 10.1 us.
   if (wave) {
     const int ks = (int)(d->nchunk < 32 ? (d->nchunk + 3) / 4 : 8);
     best = {4, ks, 1, (int)((d->nchunk + 4 * ks - 1) / (4 * ks)), 0, 0};
+    if (M == 1 && !grouped && d->nchunk > 64 && d->nchunk <= 96)
+      best = {12, (int)((d->nchunk + 11) / 12), 1, 1, 0, 0};
   }
   best.ncg = (int)((d->ntile + best.tpg - 1) / best.tpg);
   const size_t stage = (size_t)np * M * (best.ks * best.cpw * d->spc * 4 + 1) * 16;
@@ -1096,13 +1105,13 @@ int launch_gemv_wave(const sglq_dev *d, const GemvArgs &a, const Plan &pl, bool 
   const unsigned nthr = (unsigned)(waves * 64);
   switch (d->kind) {
     case SGLQ_KIND_U4:
-      launch_wave<SGLQ_KIND_U4>(a, split, d->scf16, stepm_of(d), lds, grid, nthr, st);
+      launch_wave<SGLQ_KIND_U4>(a, pl.cpw, split, d->scf16, stepm_of(d), lds, grid, nthr, st);
       break;
     case SGLQ_KIND_U8:
-      launch_wave<SGLQ_KIND_U8>(a, split, d->scf16, stepm_of(d), lds, grid, nthr, st);
+      launch_wave<SGLQ_KIND_U8>(a, pl.cpw, split, d->scf16, stepm_of(d), lds, grid, nthr, st);
       break;
     default:
-      launch_wave<SGLQ_KIND_E2M1>(a, split, 1, 0, lds, grid, nthr, st);
+      launch_wave<SGLQ_KIND_E2M1>(a, pl.cpw, split, 1, 0, lds, grid, nthr, st);
       break;
   }
   SGLQ_HIP(hipGetLastError());
@@ -1162,7 +1171,7 @@ int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows
   // (f32 gate and up halves, both 16-byte aligned), while K fits one workgroup's 8 slices
   if (max_rows == 1 && aligned && d->nchunk <= 32 &&
       (amode != 2 || (split && kcols % 4 == 0 && a_rows * lda + kcols < (1ll << 31)))) {
-    const Plan pw = plan_gemv(d, 1, split, false, true);
+    const Plan pw = plan_gemv(d, 1, split, true, true);  // 4-chunk slices
     GemvArgs aw = a;
     aw.S = pw.S;
     aw.ncg = pw.ncg;
