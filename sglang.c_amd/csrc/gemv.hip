@@ -583,7 +583,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 
 // Decode GEMV of one row (or MR = 2 rows) with wave-private activation staging: fast
 // activations (identity kmap, 16-byte aligned rows), one K slice of CPW chunks per wave (the
-// host launches CPW = 4, and 12 for one row over 65-96 chunks).
+// host launches CPW = 4, 8 and 12, the slice lengths of the one-row plan).
 // GRP 1 and 2 (MoE decode with one row per segment): blockIdx.y picks the segment, whose
 // expert supplies the weights; the row is A row r (amode 0), A row rowmap[r] (amode 1), or
 // with GRP 2 silu(A[r][k]) * A[r][kcols + k] of an f32 A; C row r is written.  (The segment
@@ -607,7 +607,10 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
   constexpr bool FOLD = SPL == 2;                  // f32: hi rows [0, M), lo rows [M, 2M)
   constexpr int RW = FOLD ? 2 : 1;                 // 128-bit words per 8-element item (and
                                                    // as many again for the up half with SWI)
-  constexpr int IPR = CPW * SPC * 4;               // items per row of a wave's slice (32..128)
+  constexpr int IPR = CPW * SPC * 4;               // items per row of a wave's slice
+  // a row's items must be whole 64-item passes, or a pass whole rows (the row maximum is
+  // reduced per pass, then over the passes of a row)
+  static_assert(IPR % 64 == 0 || 64 % IPR == 0, "slice length");
   constexpr int RS = IPR + 1;                      // LDS row stride (+1 spreads rows over banks)
   constexpr int LPR = IPR >= 64 ? 64 : IPR;        // lanes of one pass that hold the same row
   constexpr int QPR = IPR >= 64 ? IPR / 64 : 1;    // passes per row
@@ -844,11 +847,18 @@ void launch_wave(const GemvArgs &a, int cpw, bool split, int scf16, int stepm, s
       launch_wave4<KIND, 4, 2, 0, 2>(a, scf16, stepm, lds, grid, nthr, st);
     else
       launch_wave4<KIND, 4, 0, 0, 2>(a, scf16, stepm, lds, grid, nthr, st);
-  } else if (a.segs == nullptr && cpw == 12) {
+  } else if (a.segs == nullptr && cpw == 8) {
     if (split)
-      launch_wave4<KIND, 12, 2, 0>(a, scf16, stepm, lds, grid, nthr, st);
+      launch_wave4<KIND, 8, 2, 0>(a, scf16, stepm, lds, grid, nthr, st);
     else
-      launch_wave4<KIND, 12, 0, 0>(a, scf16, stepm, lds, grid, nthr, st);
+      launch_wave4<KIND, 8, 0, 0>(a, scf16, stepm, lds, grid, nthr, st);
+  } else if (a.segs == nullptr && cpw == 12) {
+    if constexpr (KIND != SGLQ_KIND_U8) {  // 8-bit codes never get 12-chunk slices
+      if (split)
+        launch_wave4<KIND, 12, 2, 0>(a, scf16, stepm, lds, grid, nthr, st);
+      else
+        launch_wave4<KIND, 12, 0, 0>(a, scf16, stepm, lds, grid, nthr, st);
+    }
   } else if (a.segs == nullptr) {
     if (split)
       launch_wave4<KIND, 4, 2, 0>(a, scf16, stepm, lds, grid, nthr, st);
@@ -998,13 +1008,22 @@ Plan plan_gemv(const sglq_dev *d, int64_t M, bool split, bool grouped = false,
   // One row through k_gemv_wave: 4-chunk slices on up to 8 waves of one tile, the rest of K
   // over workgroups.  Measured best of every (cpw 4/8, ks, tpg) with ks * tpg <= 8:
   // [11008, 4096] 8.3 us (next (8, 4, 1) 8.8), [4096, 11008] 10.0 us (next (4, 2, 1) 10.3).
-  // Over 64-96 chunks one row takes 12-chunk slices, all of K in one workgroup (no partial
-  // sums): [4096, 11008] 10.4 -> 10.1 us.
+  // One row over more chunks takes longer slices so that all of K stays in one workgroup (no
+  // partial sums): 33-64 chunks 8-chunk slices (64 chunks, against 4-chunk slices and K split
+  // in two: GPTQ4 [4096, 8192] 8.1 -> 6.8 us, GPTQ8 [4096, 4096] 7.7 -> 6.2, MXFP4 [8192, 8192]
+  // 11.9 -> 10.4), 65-96 chunks of 4-bit codes 12-chunk slices ([4096, 11008] 10.4 -> 10.1;
+  // a 12-chunk slice of 8-bit codes is not a whole number of 64-item passes).  Beyond that,
+  // 8-chunk slices with K split over workgroups.
   if (wave) {
     const int ks = (int)(d->nchunk < 32 ? (d->nchunk + 3) / 4 : 8);
     best = {4, ks, 1, (int)((d->nchunk + 4 * ks - 1) / (4 * ks)), 0, 0};
-    if (M == 1 && !grouped && d->nchunk > 64 && d->nchunk <= 96)
-      best = {12, (int)((d->nchunk + 11) / 12), 1, 1, 0, 0};
+    if (M == 1 && !grouped && d->nchunk > 32) {
+      if (d->nchunk > 64 && d->nchunk <= 96 && d->spc == 4)
+        best = {12, (int)((d->nchunk + 11) / 12), 1, 1, 0, 0};
+      else
+        best = {8, (int)(d->nchunk < 64 ? (d->nchunk + 7) / 8 : 8), 1,
+                (int)((d->nchunk + 63) / 64), 0, 0};
+    }
   }
   best.ncg = (int)((d->ntile + best.tpg - 1) / best.tpg);
   const size_t stage = (size_t)np * M * (best.ks * best.cpw * d->spc * 4 + 1) * 16;
