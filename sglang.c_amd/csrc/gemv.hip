@@ -1013,16 +1013,19 @@ Plan plan_gemv(const sglq_dev *d, int64_t M, bool split, bool grouped = false,
   // in two: GPTQ4 [4096, 8192] 8.1 -> 6.8 us, GPTQ8 [4096, 4096] 7.7 -> 6.2, MXFP4 [8192, 8192]
   // 11.9 -> 10.4), 65-96 chunks of 4-bit codes 12-chunk slices ([4096, 11008] 10.4 -> 10.1;
   // a 12-chunk slice of 8-bit codes is not a whole number of 64-item passes).  Beyond that,
-  // 8-chunk slices with K split over workgroups.
+  // 4-chunk slices, four per tile on two tiles, with K split over workgroups: best or within
+  // 0.2 us of the best in a sweep at GPTQ8 [4096, 11008], GPTQ4 [4096, 16384] and
+  // [8192, 28672], W8 [4096, 8192] (8-chunk slices on 8 waves measured up to 20% slower).
   if (wave) {
     const int ks = (int)(d->nchunk < 32 ? (d->nchunk + 3) / 4 : 8);
     best = {4, ks, 1, (int)((d->nchunk + 4 * ks - 1) / (4 * ks)), 0, 0};
     if (M == 1 && !grouped && d->nchunk > 32) {
-      if (d->nchunk > 64 && d->nchunk <= 96 && d->spc == 4)
+      if (d->nchunk <= 64)
+        best = {8, (int)((d->nchunk + 7) / 8), 1, 1, 0, 0};
+      else if (d->nchunk <= 96 && d->spc == 4)
         best = {12, (int)((d->nchunk + 11) / 12), 1, 1, 0, 0};
       else
-        best = {8, (int)(d->nchunk < 64 ? (d->nchunk + 7) / 8 : 8), 1,
-                (int)((d->nchunk + 63) / 64), 0, 0};
+        best = {4, 4, 2, (int)((d->nchunk + 15) / 16), 0, 0};
     }
   }
   best.ncg = (int)((d->ntile + best.tpg - 1) / best.tpg);

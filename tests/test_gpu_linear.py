@@ -164,7 +164,8 @@ def test_gemv_one_row_wave_staging(orc, fmt):
     """One row takes the wave-staged GEMV (each wave stages its own K slice and power of two)
     with the slice length of the one-row plan: 4 chunks up to 32 chunks (K = 2200 with a partial
     last chunk, 4096), 8 up to 64 (6000, 8192; 8-bit codes 4096), 12 over 65-96 chunks of 4-bit
-    codes (11008), and 8 with K split over workgroups beyond (16384; 8-bit codes 5120, 11008);
+    codes (11008), and 4 on two tiles with K split over workgroups beyond (16384; 8-bit codes
+    5120, 11008);
     ragged N, bias, every activation dtype."""
     u8 = fmt in ("gptq8", "w8")
     for K in ([2176, 4096, 8192, 11008, 16384] if fmt == "mxfp4" else
