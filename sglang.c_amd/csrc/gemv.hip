@@ -584,9 +584,10 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 // Decode GEMV of one row (or MR = 2 rows) with wave-private activation staging: fast
 // activations (identity kmap, 16-byte aligned rows), one K slice of CPW chunks per wave (the
 // host launches CPW = 4, 8 and 12, the slice lengths of the one-row plan).
-// GRP 1 and 2 (MoE decode with one row per segment): blockIdx.y picks the segment, whose
+// GRP 1 and 2 (MoE decode, segments of at most MR rows): blockIdx.y picks the segment, whose
 // expert supplies the weights; the row is A row r (amode 0), A row rowmap[r] (amode 1), or
-// with GRP 2 silu(A[r][k]) * A[r][kcols + k] of an f32 A; C row r is written.  (The segment
+// with GRP 2 silu(A[r][k]) * A[r][kcols + k] of an f32 A; C row r is written.  Each wave
+// stages every row of its segment, so this pays while most segments hold one row.  (The segment
 // lookups cost the one-row launches 0.8 us when they were runtime branches, so GRP is a
 // template parameter.)  Each wave loads only its own slice of the rows, takes each row's largest |a| over that
 // slice with lane shuffles, and stages the scaled f16 operands in an LDS area of its own, so no
@@ -600,7 +601,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
 // rows over K of 17-32 chunks (one workgroup range), where it measured faster.
 template <int KIND, int CPW, int SPL, bool SCF16, bool STEPM, int GRP, int MR>
 __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
-  static_assert(MR == 1 || GRP == 0, "grouped launches stage one row");
+  static_assert(MR == 1 || MR == 2 || MR == 4, "rows per launch or segment");
   constexpr bool SWI = GRP == 2;
   static_assert(!SWI || SPL == 2, "SwiGLU rows are f32");
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
@@ -864,6 +865,13 @@ void launch_wave(const GemvArgs &a, int cpw, bool split, int scf16, int stepm, s
       launch_wave4<KIND, 4, 2, 0>(a, scf16, stepm, lds, grid, nthr, st);
     else
       launch_wave4<KIND, 4, 0, 0>(a, scf16, stepm, lds, grid, nthr, st);
+  } else if (a.M > 1) {  // segments of up to 4 rows (2-4 tokens)
+    if (a.amode == 2)
+      launch_wave4<KIND, 4, 2, 2, 4>(a, scf16, stepm, lds, grid, nthr, st);
+    else if (split)
+      launch_wave4<KIND, 4, 2, 1, 4>(a, scf16, stepm, lds, grid, nthr, st);
+    else
+      launch_wave4<KIND, 4, 0, 1, 4>(a, scf16, stepm, lds, grid, nthr, st);
   } else if (a.amode == 2) {
     launch_wave4<KIND, 4, 2, 2>(a, scf16, stepm, lds, grid, nthr, st);
   } else {
@@ -1119,7 +1127,7 @@ int launch_gemv_wave(const sglq_dev *d, const GemvArgs &a, const Plan &pl, bool 
                      unsigned gy, hipStream_t st) {
   // wave-private staging: [waves][rows][IPR + 1] operands, or the slice sums
   const int64_t waves = (int64_t)pl.ks * pl.tpg;
-  const int64_t rows = (split ? 2 : 1) * a.M;  // a.M = 1 for grouped launches
+  const int64_t rows = (split ? 2 : 1) * a.M;  // a.M = most rows of a segment when grouped
   const size_t stage = (size_t)(waves * rows * (pl.cpw * d->spc * 4 + 1) * 16);
   const size_t red = (size_t)(waves * 64 * 16);
   const size_t lds = stage > red ? stage : red;
@@ -1189,9 +1197,10 @@ int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows
   a.kcols = kcols;
   const bool aligned = d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
                        (lda * esz) % 16 == 0 && a_rows * lda < (1ll << 31);
-  // one row per segment (decode of one token): the wave-staged kernel, SwiGLU rows included
-  // (f32 gate and up halves, both 16-byte aligned), while K fits one workgroup's 8 slices
-  if (max_rows == 1 && aligned && d->nchunk <= 32 &&
+  // segments of at most 4 rows (decode of 1-4 tokens): the wave-staged kernel, SwiGLU rows
+  // included (f32 gate and up halves, both 16-byte aligned), while K fits one workgroup's 8
+  // slices.  DeepSeek MoE decode (64 experts, top-6): T = 1 23.2 -> 21.7 us, T = 4 51.4 -> 43.5
+  if (max_rows <= 4 && aligned && d->nchunk <= 32 &&
       (amode != 2 || (split && kcols % 4 == 0 && a_rows * lda + kcols < (1ll << 31)))) {
     const Plan pw = plan_gemv(d, 1, split, true, true);  // 4-chunk slices
     GemvArgs aw = a;
@@ -1200,7 +1209,7 @@ int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows
     aw.ks = pw.ks;
     aw.tpg = pw.tpg;
     // the combine needs an arrival counter per tile (allocated with the split-K state)
-    if (cmb && amode == 2 && d->gv_cnt && pw.S == 1) {
+    if (cmb && max_rows == 1 && amode == 2 && d->gv_cnt && pw.S == 1) {
       aw.cpos = cmb->pos;
       aw.cw = cmb->wts;
       aw.cout = cmb->out;
