@@ -243,7 +243,8 @@ def moe_configs(torch, q, warmup, out):
         qw, qz, s = synth.gptq_expert(0x5EED0501 + 2 * e, E, mi)
         dn.append(q.QLinear.from_awq_gptq(cfg, qw, s, E, mi, qzeros=qz))
     expert_bytes = effective_bytes(2 * mi, E) + effective_bytes(E, mi)
-    for T, tag in ((512, "moe_prefill_T512_bf16"), (1, "moe_decode_T1_bf16")):
+    for T, tag in ((512, "moe_prefill_T512_bf16"), (1, "moe_decode_T1_bf16"),
+                   (4, "moe_decode_T4_bf16")):
         reps = 1 if T == 512 else 32  # decode: 32 different routings per replay (HBM-resident)
         routes = [synth.moe_routing(0x5EED0600 + r, T, n_exp, k) for r in range(reps)]
         ids = [torch.from_numpy(i).cuda() for i, _ in routes]
@@ -258,9 +259,11 @@ def moe_configs(torch, q, warmup, out):
         fl = 2 * T * k * (2 * mi * E + E * mi)
         used = len(set(np.concatenate([i.ravel() for i, _ in routes]).tolist()))
         rec = {"us": round(t * 1e6, 1), "TFLOP/s": round(fl / t / 1e12, 2)}
-        if T == 1:
-            rec["GB/s"] = round(k * expert_bytes / t / 1e9, 1)
-            rec["frac_hbm_peak"] = round(k * expert_bytes / t / 1e9 / HBM_PEAK_GBS, 4)
+        if T <= 4:
+            # weights of the distinct experts a routing selects, averaged over the routings
+            nx = np.mean([len(set(i.ravel().tolist()) - {-1}) for i, _ in routes])
+            rec["GB/s"] = round(nx * expert_bytes / t / 1e9, 1)
+            rec["frac_hbm_peak"] = round(nx * expert_bytes / t / 1e9 / HBM_PEAK_GBS, 4)
         else:
             rec["frac_f16_mfma_peak"] = round(fl / t / 1e12 / F16_PEAK_TFLOPS, 4)
             rec["experts_used"] = used
