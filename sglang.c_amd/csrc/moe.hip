@@ -97,6 +97,9 @@ __global__ __launch_bounds__(1024) void k_moe_route(const int32_t *__restrict__ 
 
 // out[t][c] = ((0 + w0 o0) + w1 o1) + ... in slot order, products and sums rounded separately
 // as the reference's orow[i] += w * o[i] (reference src/deepseek.c:675-676)
+// Up to 8 slots at a time: their rows and weights, then their products, are loaded before any
+// is added, so a token's combine costs two dependent load latencies rather than two per slot
+// (bench MoE lines: 4-token decode 45.4 -> 43.6 us, 512-token prefill 194.6 -> 191.1 us).
 __global__ void k_moe_combine(const float *__restrict__ o, int64_t ldo,
                               const int32_t *__restrict__ pos, const float *__restrict__ wts,
                               int k, int E, float *__restrict__ out) {
@@ -104,10 +107,19 @@ __global__ void k_moe_combine(const float *__restrict__ o, int64_t ldo,
   const int c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= E) return;
   float acc = 0.f;
-  for (int j = 0; j < k; j++) {
-    const int r = pos[t * k + j];
-    if (r < 0) continue;
-    acc = __fadd_rn(acc, __fmul_rn(wts[t * k + j], o[(int64_t)r * ldo + c]));
+  for (int j0 = 0; j0 < k; j0 += 8) {
+    int r[8];
+    float wv[8], v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      r[u] = j0 + u < k ? pos[t * k + j0 + u] : -1;
+      wv[u] = j0 + u < k ? wts[t * k + j0 + u] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) v[u] = r[u] >= 0 ? o[(int64_t)r[u] * ldo + c] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+      if (r[u] >= 0) acc = __fadd_rn(acc, __fmul_rn(wv[u], v[u]));
   }
   out[(int64_t)t * E + c] = acc;
 }
