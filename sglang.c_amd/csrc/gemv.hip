@@ -802,13 +802,24 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
       if (lane < 16 && n < a.N) {
         // ((0 + w0 o0) + w1 o1) + ... in slot order, as k_moe_combine (reference
         // src/deepseek.c:675-676)
+        // (8 slots at a time: rows and weights, then products, loaded before any is added)
         float sum = 0.f;
-        for (int j = 0; j < a.ck; j++) {
-          const int r = a.cpos[j];
-          if (r < 0) continue;
-          const float v = __hip_atomic_load(&a.C[(int64_t)r * a.ldc + n], __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-          sum = __fadd_rn(sum, __fmul_rn(a.cw[j], v));
+        for (int j0 = 0; j0 < a.ck; j0 += 8) {
+          int rj[8];
+          float wj[8], vj[8];
+#pragma unroll
+          for (int u = 0; u < 8; u++) {
+            rj[u] = j0 + u < a.ck ? a.cpos[j0 + u] : -1;
+            wj[u] = j0 + u < a.ck ? a.cw[j0 + u] : 0.f;
+          }
+#pragma unroll
+          for (int u = 0; u < 8; u++)
+            vj[u] = rj[u] >= 0 ? __hip_atomic_load(&a.C[(int64_t)rj[u] * a.ldc + n],
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                               : 0.f;
+#pragma unroll
+          for (int u = 0; u < 8; u++)
+            if (rj[u] >= 0) sum = __fadd_rn(sum, __fmul_rn(wj[u], vj[u]));
         }
         a.cout[n] = sum;
       }
