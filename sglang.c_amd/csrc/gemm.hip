@@ -1165,8 +1165,17 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
   const int n = (int)(blockIdx.x * 256 + threadIdx.x), m = (int)blockIdx.y;
   if (n >= N) return;
   const int64_t plane = (int64_t)M * N, o = (int64_t)m * N + n;
-  float s = part[o];
-  for (int z = 1; z < nz; z++) s += part[z * plane + o];
+  // slices added in order, 8 loads in flight at a time (one at a time, each waiting for its
+  // predecessor, the pass was latency-bound)
+  float s = 0.f;
+  for (int z0 = 0; z0 < nz; z0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) v[u] = z0 + u < nz ? part[(z0 + u) * plane + o] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+      if (z0 + u < nz) s = z0 + u == 0 ? v[u] : s + v[u];
+  }
   const int ce = colexp ? (int)colexp[n] - 127 : 0;
   C[(int64_t)m * ldc + n] = ldexpf(s, rowexp[m] + ce) + (bias ? bias[n] : 0.f);
 }
