@@ -1000,7 +1000,10 @@ Plan plan_gemv(const sglq_dev *d, int64_t M, bool split, bool grouped = false,
       const int S = (int)((d->nchunk + cpw - 1) / cpw);
       if (cpw > big) break;
       best = {cpw, 1, 8, S, 0, 0};
-      if (S <= 8) break;
+      // 16 rows: 4-chunk slices up to 16 K ranges.  [8192, 8192] M = 16 against 8-chunk
+      // slices: MXFP4 bf16 23.6 -> 20.1 us, f32 25.1 -> 22.1, GPTQ4 f32 24.7 -> 20.8, bf16
+      // 19.2 -> 19.8; at 22 ranges ([4096, 11008]) it measured 27% slower
+      if (S <= 8 || (M >= 16 && cpw == 4 && S <= 16)) break;
     }
   }
   // A short K of 9-16 chunks in one range: 4-chunk slices (more loads in flight per tile than
