@@ -287,8 +287,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
-              "quantized linear shards by output columns with no communication (see the sharding "
-              "section of DESIGN.md)", file=sys.stderr)
+              "quantized linear shards by output columns, each GPU running the same kernels on "
+              "its own tiles with no communication)", file=sys.stderr)
         sys.exit(2)
     import torch
     import synth
