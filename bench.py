@@ -34,6 +34,7 @@ HBM_PEAK_GBS = 8000.0
 F16_PEAK_TFLOPS = 2500.0  # dense bf16/fp16 MFMA (the GEMM runs v_mfma_f32_16x16x32_f16)
 FP4_PEAK_TFLOPS = 10100.0  # dense FP4 MFMA (MXFP4 GEMMs are also reported against it)
 ROTATE_BYTES = 1.1e9
+REPLAYS = 20  # timed graph replays per figure; the median is reported
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gptq_gemv_m1_traffic.txt")
 
 
@@ -59,28 +60,48 @@ def effective_bytes(N, K, G=128):
     return N * K // 2 + (K // G) * N * 2 + (K // G) * N // 2
 
 
-def time_graph(torch, body, reps, warmup):
-    """Capture body() in a graph, replay warmup + reps times; seconds per replay (HIP events on
-    the replay stream)."""
-    stream = torch.cuda.Stream()
+def capture(torch, body, stream):
+    """body() run once eagerly (sizes every workspace before capture), then captured."""
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
-        body()  # eager warm-up: sizes every workspace before capture
+        body()
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=stream):
         body()
-    for _ in range(warmup):
-        g.replay()
+    return g
+
+
+def replay_times(torch, graphs, reps, warmup, stream):
+    """Replay the graphs in turn, `warmup` untimed then `reps` timed replays, each bracketed by
+    its own pair of HIP events recorded on the replay stream; seconds per replay, in order."""
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            graphs[i % len(graphs)].replay()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(reps)]
+        torch.cuda.synchronize()
+        for i, (s, e) in enumerate(ev):
+            s.record(stream)
+            graphs[i % len(graphs)].replay()
+            e.record(stream)
     torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(reps):
-        g.replay()
-    e.record()
-    torch.cuda.synchronize()
-    return s.elapsed_time(e) / 1e3 / reps
+    return [s.elapsed_time(e) / 1e3 for s, e in ev]
+
+
+def median(xs):
+    xs = sorted(xs)
+    n = len(xs)
+    return xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2])
+
+
+def time_graph(torch, body, reps, warmup):
+    """Capture body() in a graph; median seconds per replay over max(reps, 20) replays after
+    `warmup` untimed ones (HIP events on the replay stream)."""
+    stream = torch.cuda.Stream()
+    g = capture(torch, body, stream)
+    return median(replay_times(torch, [g], max(reps, 20), warmup, stream))
 
 
 def measured_traffic():
@@ -163,7 +184,7 @@ def gemm_line(torch, ql, M, K, N, dtype, warmup, tag, out):
         out[tag]["frac_fp4_mfma_peak"] = round(fl / t / 1e12 / FP4_PEAK_TFLOPS, 4)
 
 
-EXTRA_SECTIONS = ("gemv16", "w8", "mxfp4", "gemm", "moe")
+EXTRA_SECTIONS = ("gemv16", "w8", "mxfp4", "gemm", "moe", "ceiling")
 
 
 def extra_configs(torch, q, warmup, only=EXTRA_SECTIONS):
@@ -201,7 +222,65 @@ def extra_configs(torch, q, warmup, only=EXTRA_SECTIONS):
         gemm_configs(torch, q, warmup, out)
     if "moe" in only:
         moe_configs(torch, q, warmup, out)
+    if "ceiling" in only:
+        out["ceiling"] = ceilings(torch, warmup)
     return out
+
+
+def ceilings(torch, warmup):
+    """What this box reaches with trivial kernels (sglang.c_amd/ceiling/ceiling.hip): a
+    read-only 128-bit stream at the decode GEMV's size (rotated copies) and at 1 GiB, an
+    empty launch inside a graph, and MFMA issue loops at 8 waves per SIMD on every CU.  Also
+    the vendor library's dense f16 GEMM (torch.matmul) at the M = 512 prefill shape."""
+    import ctypes as C
+    lib = C.CDLL(os.path.join(ROOT, "sglang.c_amd", "libsgl_ceiling.so"))
+    lib.sglc_stream_read.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p]
+    lib.sglc_empty.argtypes = [C.c_void_p]
+    lib.sglc_mfma.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    sink = torch.zeros(4096, dtype=torch.float32, device="cuda")
+
+    def st():
+        return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    res = {}
+    for nbytes, tag in ((23425024, "stream_read_23.4MB"), (1 << 30, "stream_read_1GiB")):
+        n16 = nbytes // 16
+        copies = max(1, math.ceil(ROTATE_BYTES / nbytes))
+        bufs = [torch.ones(n16 * 4, dtype=torch.int32, device="cuda") for _ in range(copies)]
+        for u in (8, 16):
+            def body():
+                for b in bufs:
+                    assert lib.sglc_stream_read(C.c_void_p(b.data_ptr()), n16, u,
+                                                C.c_void_p(sink.data_ptr()), st()) == 0
+            t = time_graph(torch, body, REPLAYS, warmup) / copies
+            res[f"{tag}_u{u}"] = {"GB/s": round(nbytes / t / 1e9, 1),
+                                  "frac_hbm_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4),
+                                  "us_per_launch": round(t * 1e6, 2)}
+        del bufs
+    t = time_graph(torch, lambda: [lib.sglc_empty(st()) for _ in range(200)], REPLAYS, warmup)
+    res["empty_launch_in_graph"] = {"us_per_launch": round(t / 200 * 1e6, 3)}
+    grid, iters = 256 * 8, 4096
+    for kind, tag, fl in ((0, "mfma_16x16x32_f16", 8 * 16384), (1, "mfma_16x16x32_bf16", 8 * 16384),
+                          (2, "mfma_32x32x16_f16", 4 * 32768),
+                          (3, "mfma_16x16x32_f16_builtin", 8 * 16384)):
+        t = time_graph(torch, lambda: lib.sglc_mfma(kind, grid, iters,
+                                                   C.c_void_p(sink.data_ptr()), st()),
+                       REPLAYS, warmup)
+        flops = grid * 4 * iters * fl
+        res[tag] = {"TFLOP/s": round(flops / t / 1e12, 1),
+                    "frac_f16_mfma_peak": round(flops / t / 1e12 / F16_PEAK_TFLOPS, 4),
+                    "us": round(t * 1e6, 1)}
+    import synth
+    for M in (512, 2048):
+        A = torch.from_numpy(synth.normal(0x5EED0105, (M, 4096))).cuda().half()
+        W = torch.randn(11008, 4096, device="cuda").half()
+        Cv = torch.empty((M, 11008), device="cuda", dtype=torch.half)
+        t = time_graph(torch, lambda: torch.matmul(A, W.t(), out=Cv), REPLAYS, warmup)
+        fl = 2 * M * 11008 * 4096
+        res[f"vendor_f16_gemm_M{M}_11008x4096"] = {
+            "TFLOP/s": round(fl / t / 1e12, 1),
+            "frac_f16_mfma_peak": round(fl / t / 1e12 / F16_PEAK_TFLOPS, 4),
+            "us": round(t * 1e6, 1)}
+    return res
 
 
 def gemm_configs(torch, q, warmup, out):
@@ -274,7 +353,7 @@ def moe_configs(torch, q, warmup, out):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=480)
+    ap.add_argument("--steps", type=int, default=24)
     ap.add_argument("--warmup", type=int, default=24)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
@@ -314,32 +393,52 @@ def main():
     C1 = torch.empty((1, 11008), device="cuda")
     C2 = torch.empty((1, 4096), device="cuda")
 
-    def body():
-        for g, d in zip(gates, downs):
-            g.forward(A1, out=C1)
-            d.forward(A2, out=C2)
+    # exactly K steps per graph; step i of graph j runs weight copy (j*K + i) mod copies, and
+    # the graphs cover every copy, so successive replays keep streaming distinct weights
+    K = max(1, args.steps)
+    stream = torch.cuda.Stream()
 
-    reps = max(1, args.steps // copies)
-    steps = reps * copies
-    warm = max(1, math.ceil(args.warmup / copies))
-    t_step = time_graph(torch, body, reps, warm) / copies
+    def steps_body(j, which=("gate", "down")):
+        def body():
+            for i in range(K):
+                c = (j * K + i) % copies
+                if "gate" in which:
+                    gates[c].forward(A1, out=C1)
+                if "down" in which:
+                    downs[c].forward(A2, out=C2)
+        return body
+
+    ngraph = max(1, math.ceil(copies / K))
+    reps = max(REPLAYS, ngraph)
+    warm_replays = max(1, math.ceil(args.warmup / K))
+    graphs = [capture(torch, steps_body(j), stream) for j in range(ngraph)]
+    per_replay = replay_times(torch, graphs, reps, warm_replays, stream)
+    t_step = median(per_replay) / K
+    del graphs
     value = step_bytes / t_step / 1e9
     # each shape on its own: the two launch durations of the dominant kernel
-    t_gate = time_graph(torch, lambda: [g.forward(A1, out=C1) for g in gates], reps, warm) / copies
-    t_down = time_graph(torch, lambda: [d.forward(A2, out=C2) for d in downs], reps, warm) / copies
+    t_shape = {}
+    for which in ("gate", "down"):
+        gs = [capture(torch, steps_body(j, (which,)), stream) for j in range(ngraph)]
+        t_shape[which] = median(replay_times(torch, gs, reps, warm_replays, stream)) / K
+        del gs
+    t_gate, t_down = t_shape["gate"], t_shape["down"]
     t_launch = (t_gate + t_down) / 2
     achieved = launch_bytes / t_launch / 1e9
     traffic = measured_traffic()
     res = {
         "metric": "quantized GEMV weight GB/s (% of HBM peak) at M=1; GEMM TFLOP/s at M=512",
-        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps,
-        "warmup": warm * copies, "ms_per_step": round(t_step * 1e3, 5), "higher_is_better": True,
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": round(t_step * 1e3, 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "int4 weights, f16 MFMA on f32 "
         "activations split hi+lo, fp32 accumulate",
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights GPTQ-quantized)",
         "config": {"workload": "gptq_int4_g128_gemv_llama7b_mlp_m1",
                    "weights": [[11008, 4096], [4096, 11008]], "M": 1, "act_dtype": "f32",
                    "group_size": 128, "weight_copies_rotated": copies,
+                   "timing": (f"median of {reps} graph replays of {K} steps each "
+                              f"(HIP events per replay on the replay stream), after "
+                              f"{warm_replays * K} untimed steps"),
                    "effective_weight_bytes_per_step": step_bytes},
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,

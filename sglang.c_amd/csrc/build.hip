@@ -241,23 +241,24 @@ __global__ void k_pack_meta(const uint16_t *__restrict__ dz, const float *__rest
 }
 
 // e8m0 bytes [N][nb] -> [t][16][nsteps] (step s of the device K is block s)
+// (rows of nmeta bytes; bytes past the last step are 0)
 __global__ void k_pack_e8m0(const uint8_t *__restrict__ se, int64_t N, int64_t nb, int64_t ntile,
-                            int64_t nsteps, uint8_t *__restrict__ out) {
+                            int64_t nsteps, int64_t nmeta, uint8_t *__restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= ntile * 16 * nsteps) return;
-  const int64_t tc = i / nsteps, s = i % nsteps;
+  if (i >= ntile * 16 * nmeta) return;
+  const int64_t tc = i / nmeta, s = i % nmeta;
   const int64_t n = (tc >> 4) * 16 + (tc & 15);
-  out[i] = (n < N && s < nb) ? se[n * nb + s] : (uint8_t)0;
+  out[i] = (n < N && s < nb && s < nsteps) ? se[n * nb + s] : (uint8_t)0;
 }
 
 // largest e8m0 byte of each column (255, the reference's "scale 0" code, ignored; 0 if none)
 __global__ void k_col_e8m0_max(const uint8_t *__restrict__ m, int64_t ncol, int64_t nsteps,
-                               uint8_t *__restrict__ out) {
+                               int64_t nmeta, uint8_t *__restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= ncol) return;
   uint32_t mx = 0;
   for (int64_t s = 0; s < nsteps; s++) {
-    const uint32_t e = m[i * nsteps + s];
+    const uint32_t e = m[i * nmeta + s];
     if (e != 255u && e > mx) mx = e;
   }
   out[i] = (uint8_t)mx;
@@ -286,7 +287,7 @@ __global__ void k_dequant(DqArgs a, const u32x4_t *__restrict__ codes,
   const u32x4_t blk = codes[(t * a.nchunk + c) * 64 + lane];
   if (a.kind == SGLQ_KIND_E2M1) {
     const uint32_t q = (blk[j] >> (4 * e)) & 15u;
-    const uint32_t ex = ((const uint8_t *)meta)[col * a.nsteps + s];
+    const uint32_t ex = ((const uint8_t *)meta)[col * a.nmeta + s];
     const float sc = ex == 255 ? 0.f : ldexpf(1.0f, (int)ex - 127);
     out[i] = sglq_e2m1_value(q) * sc;
     return;
@@ -349,13 +350,15 @@ static sglq_dev *build_impl(const sglq_plan *p, const void *qw, const void *qz, 
   d->nchunk = p->nsteps / d->spc;
   d->spg = p->gp / 32;
   d->ngroups = p->ngroups;
+  // meta rows are padded (e8m0 rows to 16 bytes, group entries to 4) so that the one-row
+  // GEMV reads the entries of consecutive chunks with 16-byte loads; padding entries are zero
   if (p->kind == SGLQ_KIND_E2M1) {
     d->meta_mode = SGLQ_META_E8M0;
-    d->nmeta = d->nsteps;
+    d->nmeta = (d->nsteps + 15) / 16 * 16;
   } else if (d->spg % d->spc == 0) {
     d->meta_mode = SGLQ_META_GROUP;  // every group is cpg whole chunks
     d->cpg = d->spg / d->spc;
-    d->nmeta = (d->nsteps + d->spg - 1) / d->spg;
+    d->nmeta = ((d->nsteps + d->spg - 1) / d->spg + 3) / 4 * 4;
   } else {
     d->meta_mode = SGLQ_META_STEP;
     d->nmeta = d->nsteps;
@@ -412,14 +415,14 @@ static sglq_dev *build_impl(const sglq_plan *p, const void *qw, const void *qz, 
         dc, p->N, p->K, d->kmap, p->kind, d->ntile, d->nchunk, d->codes);
     SGLQ_HIP(hipGetLastError());
     if (p->kind == SGLQ_KIND_E2M1) {
-      const int64_t nm = d->ntile * 16 * d->nsteps;
+      const int64_t nm = d->ntile * 16 * d->nmeta;
       SGLQ_HIP(hipMalloc(&d->meta, nm));
       k_pack_e8m0<<<sglq_blocks(nm, T), T>>>((const uint8_t *)b_sc, p->N, p->sc_cols, d->ntile,
-                                             d->nsteps, (uint8_t *)d->meta);
+                                             d->nsteps, d->nmeta, (uint8_t *)d->meta);
       SGLQ_HIP(hipGetLastError());
       SGLQ_HIP(hipMalloc(&d->colexp, d->ntile * 16));
-      k_col_e8m0_max<<<sglq_blocks(d->ntile * 16, T), T>>>((const uint8_t *)d->meta,
-                                                           d->ntile * 16, d->nsteps, d->colexp);
+      k_col_e8m0_max<<<sglq_blocks(d->ntile * 16, T), T>>>(
+          (const uint8_t *)d->meta, d->ntile * 16, d->nsteps, d->nmeta, d->colexp);
       SGLQ_HIP(hipGetLastError());
     } else {
       const int64_t GN = p->ngroups * p->N;
@@ -549,7 +552,10 @@ extern "C" int64_t sglq_N(const sglq_dev *d) { return d->N; }
 extern "C" int64_t sglq_K(const sglq_dev *d) { return d->K; }
 extern "C" int64_t sglq_weight_bytes(const sglq_dev *d) {
   const int64_t codes = d->ntile * d->nchunk * 1024;
-  const int64_t nm = d->ntile * 16 * d->nmeta;
+  // entries a forward reads (the row padding is never read)
+  const int64_t nm = d->ntile * 16 *
+                     (d->meta_mode == SGLQ_META_GROUP ? (d->nsteps + d->spg - 1) / d->spg
+                                                      : d->nsteps);
   if (d->kind == SGLQ_KIND_E2M1) return codes + nm;
   return codes + nm * (d->scf16 ? 4 : 8);
 }

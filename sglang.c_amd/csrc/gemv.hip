@@ -19,9 +19,12 @@
 // row by an exact power of two so it sits well inside f16 range; f32 inputs are split into f16
 // hi + lo parts (about 22 significant bits), bf16/f16 inputs fit one f16 part.  The power of
 // two is undone exactly on the result.
+#include <stdlib.h>
 #include <string.h>
 
-#include "sglq_dev.hpp"
+#include "gemv_ops.hpp"
+
+using namespace sglq;
 
 namespace {
 
@@ -54,10 +57,6 @@ struct GemvArgs {
   int ck;
 };
 
-__device__ __forceinline__ float bf16_bits(uint32_t b) { return __uint_as_float(b << 16); }
-__device__ __forceinline__ float f16_bits(uint32_t b) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)b);
-}
 
 __device__ __forceinline__ float act1(const void *A, int dt, int64_t i) {
   if (dt == SGLQ_DT_F32) return ((const float *)A)[i];
@@ -95,75 +94,6 @@ __device__ __forceinline__ void load8(const GemvArgs &a, int64_t row, int kp, fl
   }
 }
 
-// (x & m) | o as one v_and_or_b32 (the compiler otherwise emits an AND and an OR)
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(o));
-  return r;
-}
-
-union H8 {
-  half8_t v;
-  uint32_t u[4];
-  half2_t h[4];
-};
-
-// Codes of step j of a chunk -> B operand.  U4 element order is nibbles {0,4,1,5,2,6,3,7}:
-// (x & 0x000F000F) | 0x6400 gives 1024 + q, (x & 0x00F000F0) | 0x5400 gives 64 + q, and the
-// matching exact offsets zA = -(1024 + z), zB = -(64 + z) leave q - z.
-template <int KIND>
-__device__ __forceinline__ half8_t unpack(const u32x4_t &w, int j, half2_t zA, half2_t zB) {
-  H8 r;
-  if constexpr (KIND == SGLQ_KIND_U4) {
-    const uint32_t x = w[j], y = x >> 8;
-    r.u[0] = and_or(x, 0x000F000Fu, 0x64006400u);
-    r.u[1] = and_or(x, 0x00F000F0u, 0x54005400u);
-    r.u[2] = and_or(y, 0x000F000Fu, 0x64006400u);
-    r.u[3] = and_or(y, 0x00F000F0u, 0x54005400u);
-    r.h[0] = r.h[0] + zA;
-    r.h[1] = r.h[1] + zB;
-    r.h[2] = r.h[2] + zA;
-    r.h[3] = r.h[3] + zB;
-  } else if constexpr (KIND == SGLQ_KIND_U8) {
-    const uint32_t x0 = w[2 * j], x1 = w[2 * j + 1];
-    r.u[0] = __builtin_amdgcn_perm(0x64646464u, x0, 0x04010400u);  // 1024 + b0, 1024 + b1
-    r.u[1] = __builtin_amdgcn_perm(0x64646464u, x0, 0x04030402u);
-    r.u[2] = __builtin_amdgcn_perm(0x64646464u, x1, 0x04010400u);
-    r.u[3] = __builtin_amdgcn_perm(0x64646464u, x1, 0x04030402u);
-#pragma unroll
-    for (int i = 0; i < 4; i++) r.h[i] = r.h[i] + zA;
-  } else {
-    const uint32_t x = w[j];
-    r.h[0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(x, 1.0f, 0);
-    r.h[1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(x, 1.0f, 1);
-    r.h[2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(x, 1.0f, 2);
-    r.h[3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(x, 1.0f, 3);
-  }
-  return r.v;
-}
-
-template <bool SCF16>
-using meta_t = typename std::conditional<SCF16, uint32_t, uint64_t>::type;
-
-template <bool SCF16>
-__device__ __forceinline__ void decode_meta(meta_t<SCF16> m, float &sc, half2_t &zA,
-                                            half2_t &zB) {
-  uint32_t zb;
-  if constexpr (SCF16) {
-    sc = f16_bits(m & 0xFFFFu);
-    zb = m >> 16;
-  } else {
-    sc = __uint_as_float((uint32_t)m);
-    zb = (uint32_t)(m >> 32) & 0xFFFFu;
-  }
-  const _Float16 z = __builtin_bit_cast(_Float16, (uint16_t)zb);
-  zA = (half2_t){z, z};
-  const _Float16 z2 = z + (_Float16)960.0f;  // -(64 + zero), exact
-  zB = (half2_t){z2, z2};
-}
-
-// element i of a U4 operand holds k-offset {0,4,1,5,2,6,3,7}[i]
-__device__ __forceinline__ constexpr int kofs4(int i) { return (i >> 1) + 4 * (i & 1); }
 
 // Split-K epilogue of a decode GEMV workgroup whose partial sums are stored: the last
 // workgroup of the column group (the last wave of the tile when a.ks > 1, after the other
@@ -1166,6 +1096,15 @@ fail:
 
 }  // namespace
 
+// SGLQ_GEMV_ROW=0 in the environment keeps one-row launches on k_gemv_wave (A/B measurement)
+static bool sglq_gemv_row_off() {
+  static const int off = [] {
+    const char *v = getenv("SGLQ_GEMV_ROW");
+    return v && v[0] == '0' ? 1 : 0;
+  }();
+  return off != 0;
+}
+
 int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
               float *C, int64_t ldc, hipStream_t st) {
   const bool split = dt == SGLQ_DT_F32;
@@ -1175,6 +1114,10 @@ int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
   // two rows only while K fits one workgroup range: [11008, 4096] 11.2 -> 9.8 us (f32), 10.2 ->
   // 9.7 (bf16); with K split over workgroups ([4096, 11008]) it measured equal or slower
   const bool wave = fast && (M == 1 || (M == 2 && d->nchunk > 16 && d->nchunk <= 32));
+  if (M == 1 && fast && !sglq_gemv_row_off()) {
+    const int r = sglq_gemv_row(d, A, dt, bias, C, st);
+    if (r != 0) return r == 1 ? 0 : -1;
+  }
   const Plan pl = plan_gemv(d, M, split, false, wave);
   if (pl.S > d->gv_split) {
     sglq_log_error("qlinear: GEMV split %d exceeds its state (%d)", pl.S, d->gv_split);

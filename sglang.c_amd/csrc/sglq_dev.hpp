@@ -91,6 +91,10 @@ int sglq_ws_reserve(sglq_dev *d, size_t bytes);
 // Decode-GEMV launch (gemv.hip): C rows [0, M) with M <= 16.
 int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
               float *C, int64_t ldc, hipStream_t st);
+// One-row decode GEMV (gemv_row.hip): 1 = launched, 0 = not applicable to this weight / row
+// (the caller takes sglq_gemv), -1 = launch error.
+int sglq_gemv_row(const sglq_dev *d, const void *A, int dt, const float *bias, float *C,
+                  hipStream_t st);
 // Prefill GEMM launch (gemm.hip): any M; grows the handle's workspace on first use at a size.
 int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
               float *C, int64_t ldc, hipStream_t st);
