@@ -215,14 +215,15 @@ __global__ void k_pack_codes(const uint8_t *__restrict__ dc, int64_t N, int64_t 
 }
 
 // Per-(tile, column, unit) meta entries (layout in sglq_dev.hpp).  A unit is group u
-// (META_GROUP) or step u, whose group is u / spg (META_STEP).
+// (META_GROUP) or step u, whose group is u / spg (META_STEP).  Thread i writes entry i.
 __global__ void k_pack_meta(const uint16_t *__restrict__ dz, const float *__restrict__ ds,
                             int64_t N, int64_t ngroups, int64_t ntile, int64_t nmeta,
                             int64_t upg, int f16, void *__restrict__ om) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= ntile * 16 * nmeta) return;
-  const int64_t tc = i / nmeta, u = i % nmeta;
-  const int64_t n = (tc >> 4) * 16 + (tc & 15);
+  const int64_t t = i / (16 * nmeta), r = i % (16 * nmeta);
+  const int64_t u = (r >> 6) * 4 + (r & 3);
+  const int64_t n = t * 16 + ((r >> 2) & 15);
   const int64_t g = u / upg;
   float s = 0.f;
   int z = 0;
@@ -240,14 +241,15 @@ __global__ void k_pack_meta(const uint16_t *__restrict__ dz, const float *__rest
   }
 }
 
-// e8m0 bytes [N][nb] -> [t][16][nsteps] (step s of the device K is block s)
-// (rows of nmeta bytes; bytes past the last step are 0)
+// e8m0 bytes [N][nb] -> the quad layout of sglq_ebyte (step s of the device K is block s;
+// bytes past the last step are 0).  Thread i writes byte i.
 __global__ void k_pack_e8m0(const uint8_t *__restrict__ se, int64_t N, int64_t nb, int64_t ntile,
                             int64_t nsteps, int64_t nmeta, uint8_t *__restrict__ out) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= ntile * 16 * nmeta) return;
-  const int64_t tc = i / nmeta, s = i % nmeta;
-  const int64_t n = (tc >> 4) * 16 + (tc & 15);
+  const int64_t t = i / (16 * nmeta), r = i % (16 * nmeta);
+  const int64_t s = (r >> 8) * 16 + (r & 15);
+  const int64_t n = t * 16 + ((r >> 4) & 15);
   out[i] = (n < N && s < nb && s < nsteps) ? se[n * nb + s] : (uint8_t)0;
 }
 
@@ -258,7 +260,7 @@ __global__ void k_col_e8m0_max(const uint8_t *__restrict__ m, int64_t ncol, int6
   if (i >= ncol) return;
   uint32_t mx = 0;
   for (int64_t s = 0; s < nsteps; s++) {
-    const uint32_t e = m[i * nmeta + s];
+    const uint32_t e = m[sglq_ebyte(i >> 4, (int)(i & 15), s, nmeta)];
     if (e != 255u && e > mx) mx = e;
   }
   out[i] = (uint8_t)mx;
@@ -281,13 +283,13 @@ __global__ void k_dequant(DqArgs a, const u32x4_t *__restrict__ codes,
   const int64_t n = i / a.K, k = i % a.K;
   const int64_t kp = kinv[k];
   const int64_t s = kp >> 5, c = s / a.spc, j = s % a.spc;
-  const int64_t t = n >> 4, col = (t << 4) + (n & 15);  // == n; meta rows are [t][16]
+  const int64_t t = n >> 4;
   const int lane = (int)(((kp & 31) >> 3) * 16 + (n & 15));
   const int e = (int)(kp & 7);
   const u32x4_t blk = codes[(t * a.nchunk + c) * 64 + lane];
   if (a.kind == SGLQ_KIND_E2M1) {
     const uint32_t q = (blk[j] >> (4 * e)) & 15u;
-    const uint32_t ex = ((const uint8_t *)meta)[col * a.nmeta + s];
+    const uint32_t ex = ((const uint8_t *)meta)[sglq_ebyte(t, (int)(n & 15), s, a.nmeta)];
     const float sc = ex == 255 ? 0.f : ldexpf(1.0f, (int)ex - 127);
     out[i] = sglq_e2m1_value(q) * sc;
     return;
@@ -298,7 +300,7 @@ __global__ void k_dequant(DqArgs a, const u32x4_t *__restrict__ codes,
   else
     q = (blk[j] >> (4 * e)) & 15u;
   const int64_t u = a.meta_mode == SGLQ_META_GROUP ? c / a.cpg : s;
-  const int64_t mi = col * a.nmeta + u;
+  const int64_t mi = sglq_mrow(t, (int)(n & 15), a.nmeta) + sglq_mofs(u);
   float sc;
   uint16_t zb;
   if (a.scf16) {
@@ -361,7 +363,7 @@ static sglq_dev *build_impl(const sglq_plan *p, const void *qw, const void *qz, 
     d->nmeta = ((d->nsteps + d->spg - 1) / d->spg + 3) / 4 * 4;
   } else {
     d->meta_mode = SGLQ_META_STEP;
-    d->nmeta = d->nsteps;
+    d->nmeta = (d->nsteps + 3) / 4 * 4;
   }
   d->kident = 1;
   for (int64_t k = 0; k < p->K && d->kident; k++) d->kident = p->kmap[k] == k;

@@ -477,8 +477,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
   for (int j = 0; j < TN; j++) {
     const int t = min(t0 + j, a.ntile - 1);
     bptr[j] = codes + (int64_t)t * a.nchunk * 64 + lane;
-    mptr[j] = (const MT *)((const char *)meta +
-                           ((int64_t)t * 16 + n16) * a.nmeta * (E2M1 ? 1 : (int)sizeof(MT)));
+    mptr[j] = (const MT *)meta + sglq_mrow(t, n16, E2M1 ? a.nmeta / 4 : a.nmeta);
   }
   u32x4_t bw[TN];
   MT bm_[TN][NMV];
@@ -493,12 +492,12 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     for (int j = 0; j < TN; j++) {
       w_[j] = ldg_nt(bptr[j] + c * 64);
       if constexpr (E2M1) {
-        m_[j][0] = ldg((const uint32_t *)mptr[j] + c);
+        m_[j][0] = ldg((const uint32_t *)mptr[j] + sglq_mofs(c));
       } else if constexpr (STEPM) {
 #pragma unroll
-        for (int s = 0; s < SPC; s++) m_[j][s] = ldg(mptr[j] + c * SPC + s);
+        for (int s = 0; s < SPC; s++) m_[j][s] = ldg(mptr[j] + sglq_mofs(c * SPC + s));
       } else {
-        m_[j][0] = ldg(mptr[j] + g);
+        m_[j][0] = ldg(mptr[j] + sglq_mofs(g));
       }
     }
   };
@@ -815,8 +814,7 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
       t = min(bn * NT16 + tb, a.ntile - 1);
     }
     bsrc[q] = codes + (int64_t)t * a.nchunk * 64 + lb;
-    msrc[q] = (const uint32_t *)((const char *)meta +
-                                 ((int64_t)t * 16 + (lb & 15)) * a.nmeta * (E2M1 ? 1 : 4));
+    msrc[q] = (const uint32_t *)meta + sglq_mrow(t, lb & 15, E2M1 ? a.nmeta / 4 : a.nmeta);
     if constexpr (E2M1) cref[q] = colexp[t * 16 + (lb & 15)];
   }
   auto load_b = [&](int st, u32x4_t(&breg)[PB], MT(&mreg)[PB]) {
@@ -834,9 +832,9 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
         breg[q] = (u32x4_t){x[0], x[1], 0u, 0u};
       }
       if constexpr (E2M1)
-        mreg[q] = ldg(msrc[q] + c) >> (8 * SS * h);  // e8m0 bytes of the stage's steps
+        mreg[q] = ldg(msrc[q] + sglq_mofs(c)) >> (8 * SS * h);  // e8m0 bytes of the stage's steps
       else
-        mreg[q] = ldg(msrc[q] + g);
+        mreg[q] = ldg(msrc[q] + sglq_mofs(g));
     }
   };
   auto store_b = [&](int buf, const u32x4_t(&breg)[PB], const MT(&mreg)[PB]) {
@@ -1056,15 +1054,15 @@ __global__ __launch_bounds__(64 * WN, 2) void k_gemm_breg(GemmArgs a) {
       t = min(bn * NT16 + wn * TN + j, a.ntile - 1);
     }
     bsrc[j] = codes + (int64_t)t * a.nchunk * 64 + lane;
-    msrc[j] = (const uint32_t *)((const char *)meta +
-                                 ((int64_t)t * 16 + n16) * a.nmeta * (E2M1 ? 1 : 4));
+    msrc[j] = (const uint32_t *)meta + sglq_mrow(t, n16, E2M1 ? a.nmeta / 4 : a.nmeta);
     cref[j] = E2M1 ? colexp[t * 16 + n16] : 0;
   }
   auto load_b = [&](int c, u32x4_t(&bw)[TN], uint32_t(&bm_)[TN]) {
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       bw[j] = ldg_nt(bsrc[j] + c * 64);
-      bm_[j] = E2M1 ? ldg(msrc[j] + c) : ldg(msrc[j] + c / a.cpg);  // e8m0 bytes | group meta
+      // e8m0 bytes | group meta
+      bm_[j] = E2M1 ? ldg(msrc[j] + sglq_mofs(c)) : ldg(msrc[j] + sglq_mofs(c / a.cpg));
     }
   };
 

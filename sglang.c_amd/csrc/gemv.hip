@@ -176,23 +176,23 @@ struct WaveWeights {
   __device__ __forceinline__ void load(const GemvArgs &a, const u32x4_t *codes, const void *meta,
                                        int tl, int n16, int lane, int c0) {
     const int clast = a.nchunk - 1;
-    const int64_t mrow = ((int64_t)tl * 16 + n16) * a.nmeta;
     if constexpr (E2M1) {
-      const uint32_t *ep = (const uint32_t *)((const uint8_t *)meta + mrow);
+      const uint32_t *ep = (const uint32_t *)meta + sglq_mrow(tl, n16, a.nmeta / 4);
 #pragma unroll
-      for (int i = 0; i < CPW; i++) mv[i] = ep[min(c0 + i, clast)];
+      for (int i = 0; i < CPW; i++) mv[i] = ep[sglq_mofs(min(c0 + i, clast))];
     } else if constexpr (STEPM) {
-      const MT *mp = (const MT *)meta + mrow;
+      const MT *mp = (const MT *)meta + sglq_mrow(tl, n16, a.nmeta);
 #pragma unroll
-      for (int i = 0; i < CPW * SPC; i++) mv[i] = mp[min(c0 * SPC + i, clast * SPC + SPC - 1)];
+      for (int i = 0; i < CPW * SPC; i++)
+        mv[i] = mp[sglq_mofs(min(c0 * SPC + i, clast * SPC + SPC - 1))];
     } else {
-      const MT *mp = (const MT *)meta + mrow;
+      const MT *mp = (const MT *)meta + sglq_mrow(tl, n16, a.nmeta);
       const int cc = min(c0, clast);
       int g = cc / a.cpg, r = cc - g * a.cpg;
       const int glast = clast / a.cpg;
 #pragma unroll
       for (int i = 0; i < CPW; i++) {
-        mv[i] = mp[min(g, glast)];
+        mv[i] = mp[sglq_mofs(min(g, glast))];
         if (++r == a.cpg) {
           r = 0;
           g++;

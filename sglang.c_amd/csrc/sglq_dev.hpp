@@ -11,12 +11,17 @@
 //     step.  4-bit kinds: a chunk is 4 steps, word j of the lane is step 4c+j, nibble i holds
 //     k-offset i.  8-bit kind: a chunk is 2 steps, words (2j, 2j+1) are step 2c+j, byte b of
 //     the pair holds k-offset b.
-//   * U4/U8 meta, one entry per (tile, column, unit) stored [t][16][nmeta]; a unit is a group
-//     when every group is a whole number of chunks (META_GROUP, cpg chunks per group), else a
-//     step (META_STEP).  Entry = f16 scale | f16 -(1024 + zero) << 16 when every scale is
-//     f16-exact (4 bytes), else f32 scale | f16 -(1024 + zero) << 32 (8 bytes).
-//   * E2M1 meta: the e8m0 byte of every (column, step), stored [t][16][nsteps] (u8), plus the
-//     largest of them per column (colexp), the reference exponent of the prefill GEMM.
+//   * U4/U8 meta, one entry per (tile, column, unit); a unit is a group when every group is a
+//     whole number of chunks (META_GROUP, cpg chunks per group), else a step (META_STEP).
+//     Entry = f16 scale | f16 -(1024 + zero) << 16 when every scale is f16-exact (4 bytes),
+//     else f32 scale | f16 -(1024 + zero) << 32 (8 bytes).  nmeta units per column, padded to
+//     a multiple of 4 (padding entries are zero), stored in quads: the entries of units
+//     4v .. 4v+3 of the tile's 16 columns are contiguous, [t][v][16][4], so one wave's
+//     entries of four consecutive units are one contiguous run (sglq_mrow / sglq_mofs).
+//   * E2M1 meta: the e8m0 byte of every (column, step), nmeta bytes per column (padded to a
+//     multiple of 16), in the same quads of 4-byte words (one word = the four steps of a
+//     chunk): [t][v][16][16 bytes]; plus the largest byte per column (colexp), the reference
+//     exponent of the prefill GEMM.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -145,6 +150,18 @@ int sglq_gemv_grouped(const sglq_dev *d, const struct sglq_group *grp, int64_t m
                       hipStream_t st, const sglq_combine *cmb = nullptr);
 // Picks the decode GEMV split for a freshly built weight and allocates its state.
 int sglq_gemv_setup(sglq_dev *d);
+
+// Meta entry (tile t, column n16 of the tile, unit u) = row base + offset, in entries (4 or 8
+// bytes; for E2M1 4-byte words, u = chunk, nm = nmeta / 4); nm = entries per column.
+__host__ __device__ __forceinline__ int64_t sglq_mrow(int64_t t, int n16, int64_t nm) {
+  return t * nm * 16 + n16 * 4;
+}
+__host__ __device__ __forceinline__ int64_t sglq_mofs(int64_t u) { return (u >> 2) * 64 + (u & 3); }
+// e8m0 byte of (tile t, column n16, step s), nmeta bytes per column
+__host__ __device__ __forceinline__ int64_t sglq_ebyte(int64_t t, int n16, int64_t s,
+                                                      int64_t nmeta) {
+  return t * nmeta * 16 + (s >> 4) * 256 + n16 * 16 + (s & 15);
+}
 
 __device__ __forceinline__ float sglq_e2m1_value(uint32_t c) {
   // reference src/qweight.c:325-329
