@@ -28,7 +28,7 @@ import sys
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
-sys.path[:0] = [ROOT, os.path.join(ROOT, "sglang.c_amd")]
+sys.path[:0] = [ROOT, os.path.join(ROOT, "sglang.c_amd"), os.path.join(ROOT, "tests")]
 
 HBM_PEAK_GBS = 8000.0
 F16_PEAK_TFLOPS = 2500.0  # dense bf16/fp16 MFMA (the GEMM runs v_mfma_f32_16x16x32_f16)

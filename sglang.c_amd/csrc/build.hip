@@ -494,34 +494,51 @@ extern "C" void sglq_free(sglq_dev *d) {
   (void)hipFree(d->kinv);
   (void)hipFree(d->ws);
   (void)hipFree(d->aux);
+  for (int i = 0; i < d->nretired; i++) (void)hipFree(d->retired[i]);
+  free(d->retired);
   free(d->moe_tbl);
   free(d);
 }
 
-int sglq_ws_reserve(sglq_dev *d, size_t bytes) {
-  if (d->ws_bytes >= bytes) return 0;
-  (void)hipFree(d->ws);
-  d->ws = nullptr;
-  d->ws_bytes = 0;
-  if (hipMalloc(&d->ws, bytes) != hipSuccess) {
-    sglq_log_error("workspace allocation of %zu bytes failed", bytes);
-    return -1;
+// A buffer outgrown by a larger call is retired, not freed: a HIP graph captured from an
+// earlier call on this handle still holds its address, so it stays allocated until
+// sglq_free.
+static int retire(sglq_dev *d, void *p) {
+  if (!p) return 0;
+  if (d->nretired == d->cap_retired) {
+    const int cap = d->cap_retired ? 2 * d->cap_retired : 8;
+    void **r = (void **)realloc(d->retired, sizeof(void *) * (size_t)cap);
+    if (!r) return -1;
+    d->retired = r;
+    d->cap_retired = cap;
   }
-  d->ws_bytes = bytes;
+  d->retired[d->nretired++] = p;
   return 0;
 }
 
-int sglq_aux_reserve(sglq_dev *d, size_t bytes) {
-  if (d->aux_bytes >= bytes) return 0;
-  (void)hipFree(d->aux);
-  d->aux = nullptr;
-  d->aux_bytes = 0;
-  if (hipMalloc(&d->aux, bytes) != hipSuccess) {
-    sglq_log_error("auxiliary buffer allocation of %zu bytes failed", bytes);
+static int grow(sglq_dev *d, void **buf, size_t *have, size_t bytes, const char *what) {
+  if (*have >= bytes) return 0;
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) {
+    sglq_log_error("%s allocation of %zu bytes failed", what, bytes);
     return -1;
   }
-  d->aux_bytes = bytes;
+  if (retire(d, *buf) != 0) {
+    (void)hipFree(p);
+    sglq_log_error("%s: out of host memory", what);
+    return -1;
+  }
+  *buf = p;
+  *have = bytes;
   return 0;
+}
+
+int sglq_ws_reserve(sglq_dev *d, size_t bytes) {
+  return grow(d, &d->ws, &d->ws_bytes, bytes, "workspace");
+}
+
+int sglq_aux_reserve(sglq_dev *d, size_t bytes) {
+  return grow(d, &d->aux, &d->aux_bytes, bytes, "auxiliary buffer");
 }
 
 extern "C" int sglq_dequant_dev(sglq_dev *d, float *out, void *stream) {

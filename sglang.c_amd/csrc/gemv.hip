@@ -1202,26 +1202,3 @@ fail:
   return -1;
 }
 
-extern "C" int sglq_forward_host(sglq_dev *d, const float *A, int64_t M, const float *bias,
-                                 float *C) {
-  float *dA = nullptr, *dB = nullptr, *dC = nullptr;
-  SGLQ_HIP(hipSetDevice(d->dev));
-  SGLQ_HIP(hipMalloc(&dA, (size_t)(M * d->K) * 4));
-  SGLQ_HIP(hipMalloc(&dC, (size_t)(M * d->N) * 4));
-  SGLQ_HIP(hipMemcpy(dA, A, (size_t)(M * d->K) * 4, hipMemcpyHostToDevice));
-  if (bias) {
-    SGLQ_HIP(hipMalloc(&dB, (size_t)d->N * 4));
-    SGLQ_HIP(hipMemcpy(dB, bias, (size_t)d->N * 4, hipMemcpyHostToDevice));
-  }
-  if (sglq_forward(d, dA, SGLQ_DT_F32, M, dB, dC, nullptr) != 0) goto fail;
-  SGLQ_HIP(hipMemcpy(C, dC, (size_t)(M * d->N) * 4, hipMemcpyDeviceToHost));
-  (void)hipFree(dA);
-  (void)hipFree(dB);
-  (void)hipFree(dC);
-  return 0;
-fail:
-  (void)hipFree(dA);
-  (void)hipFree(dB);
-  (void)hipFree(dC);
-  return -1;
-}

@@ -82,80 +82,22 @@ __global__ __launch_bounds__(256) void k_matmul_nt(const float *__restrict__ A,
   }
 }
 
-extern "C" int sglq_quant_rows_i8_host(const float *x, int8_t *out, float *scales, int64_t rows,
-                                       int64_t dim) {
-  float *dx = nullptr, *ds = nullptr;
-  int8_t *dq = nullptr;
-  const size_t n = (size_t)(rows * dim);
-  if (rows <= 0 || dim <= 0) return 0;
-  SGLQ_HIP(hipMalloc(&dx, n * 4));
-  SGLQ_HIP(hipMalloc(&dq, n));
-  SGLQ_HIP(hipMalloc(&ds, (size_t)rows * 4));
-  SGLQ_HIP(hipMemcpy(dx, x, n * 4, hipMemcpyHostToDevice));
-  k_quant_rows_i8<<<(unsigned)rows, 256>>>(dx, dq, ds, dim);
-  SGLQ_HIP(hipGetLastError());
-  SGLQ_HIP(hipMemcpy(out, dq, n, hipMemcpyDeviceToHost));
-  SGLQ_HIP(hipMemcpy(scales, ds, (size_t)rows * 4, hipMemcpyDeviceToHost));
-  (void)hipFree(dx);
-  (void)hipFree(dq);
-  (void)hipFree(ds);
-  return 0;
-fail:
-  (void)hipFree(dx);
-  (void)hipFree(dq);
-  (void)hipFree(ds);
-  return -1;
+// launches for the host-buffer entry points (hostio.hip)
+int sglq_launch_quant_rows_i8(const float *x, int8_t *q, float *scales, int64_t rows,
+                              int64_t dim, hipStream_t st) {
+  k_quant_rows_i8<<<(unsigned)rows, 256, 0, st>>>(x, q, scales, dim);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
-
-extern "C" int sglq_dequant_row_i8_host(const int8_t *q, float scale, float *out, int64_t n) {
-  int8_t *dq = nullptr;
-  float *dout = nullptr;
-  if (n <= 0) return 0;
-  SGLQ_HIP(hipMalloc(&dq, (size_t)n));
-  SGLQ_HIP(hipMalloc(&dout, (size_t)n * 4));
-  SGLQ_HIP(hipMemcpy(dq, q, (size_t)n, hipMemcpyHostToDevice));
-  k_dequant_row_i8<<<sglq_blocks(n, 256), 256>>>(dq, scale, dout, n);
-  SGLQ_HIP(hipGetLastError());
-  SGLQ_HIP(hipMemcpy(out, dout, (size_t)n * 4, hipMemcpyDeviceToHost));
-  (void)hipFree(dq);
-  (void)hipFree(dout);
-  return 0;
-fail:
-  (void)hipFree(dq);
-  (void)hipFree(dout);
-  return -1;
+int sglq_launch_dequant_row_i8(const int8_t *q, float scale, float *o, int64_t n,
+                               hipStream_t st) {
+  k_dequant_row_i8<<<sglq_blocks(n, 256), 256, 0, st>>>(q, scale, o, n);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
-
-extern "C" int sglq_matmul_nt_host(const float *A, const float *W, const float *bias, float *C,
-                                   int64_t M, int64_t N, int64_t K) {
-  float *dA = nullptr, *dW = nullptr, *dB = nullptr, *dC = nullptr;
-  if (M <= 0 || N <= 0) return 0;
-  SGLQ_HIP(hipMalloc(&dA, (size_t)(M * K) * 4));
-  SGLQ_HIP(hipMalloc(&dW, (size_t)(N * K) * 4));
-  SGLQ_HIP(hipMalloc(&dC, (size_t)(M * N) * 4));
-  SGLQ_HIP(hipMemcpy(dA, A, (size_t)(M * K) * 4, hipMemcpyHostToDevice));
-  SGLQ_HIP(hipMemcpy(dW, W, (size_t)(N * K) * 4, hipMemcpyHostToDevice));
-  if (bias) {
-    SGLQ_HIP(hipMalloc(&dB, (size_t)N * 4));
-    SGLQ_HIP(hipMemcpy(dB, bias, (size_t)N * 4, hipMemcpyHostToDevice));
-  }
-  {
-    const int64_t waves = N * ((M + 7) / 8);
-    k_matmul_nt<<<sglq_blocks(waves * 64, 256), 256>>>(dA, dW, dB, dC, M, N, K);
-  }
-  SGLQ_HIP(hipGetLastError());
-  SGLQ_HIP(hipMemcpy(C, dC, (size_t)(M * N) * 4, hipMemcpyDeviceToHost));
-  (void)hipFree(dA);
-  (void)hipFree(dW);
-  (void)hipFree(dB);
-  (void)hipFree(dC);
-  return 0;
-fail:
-  (void)hipFree(dA);
-  (void)hipFree(dW);
-  (void)hipFree(dB);
-  (void)hipFree(dC);
-  return -1;
+int sglq_launch_matmul_nt(const float *A, const float *W, const float *bias, float *C,
+                          int64_t M, int64_t N, int64_t K, hipStream_t st) {
+  const int64_t waves = N * ((M + 7) / 8);
+  k_matmul_nt<<<sglq_blocks(waves * 64, 256), 256, 0, st>>>(A, W, bias, C, M, N, K);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 // out[r][i] = (float)q[r][i] * scales[r]: sgl_dequant_row_i8 over rows

@@ -69,6 +69,10 @@ struct sglq_dev {
   // from ws, which the forwards inside that pass use)
   void *aux;
   size_t aux_bytes;
+  // buffers outgrown by ws / aux, kept until the handle is freed (graphs captured earlier may
+  // still reference them)
+  void **retired;
+  int nretired, cap_retired;
   // MoE: host copy of the expert pointer table last uploaded into ws (re-uploaded on change)
   void *moe_tbl;
   size_t moe_tbl_bytes;
@@ -89,7 +93,8 @@ static inline unsigned sglq_blocks(int64_t n, int threads) {
   return (unsigned)((n + threads - 1) / threads);
 }
 
-// Grows d->ws to at least `bytes` (device memory, kept for the handle's lifetime).
+// Grow d->ws / d->aux to at least `bytes` (device memory; an outgrown buffer stays allocated
+// until the handle is freed, since a graph captured earlier may hold its address).
 int sglq_aux_reserve(sglq_dev *d, size_t bytes);
 int sglq_ws_reserve(sglq_dev *d, size_t bytes);
 
@@ -100,6 +105,13 @@ int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
 // (the caller takes sglq_gemv), -1 = launch error.
 int sglq_gemv_row(const sglq_dev *d, const void *A, int dt, const float *bias, float *C,
                   hipStream_t st);
+// Kernels behind the host-buffer entry points (int8.hip), launched on st.
+int sglq_launch_quant_rows_i8(const float *x, int8_t *q, float *scales, int64_t rows,
+                              int64_t dim, hipStream_t st);
+int sglq_launch_dequant_row_i8(const int8_t *q, float scale, float *o, int64_t n,
+                               hipStream_t st);
+int sglq_launch_matmul_nt(const float *A, const float *W, const float *bias, float *C,
+                          int64_t M, int64_t N, int64_t K, hipStream_t st);
 // Prefill GEMM launch (gemm.hip): any M; grows the handle's workspace on first use at a size.
 int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
               float *C, int64_t ldc, hipStream_t st);

@@ -79,12 +79,16 @@ int64_t sglq_K(const sglq_dev *d);
 /* bytes of the device layout that one forward streams (codes + scales + zeros) */
 int64_t sglq_weight_bytes(const sglq_dev *d);
 
-/* int8 row quantization and f32 NT matmul on host buffers, computed on the GPU. */
+/* int8 row quantization on host buffers, computed on the GPU (device 0). */
 int sglq_quant_rows_i8_host(const float *x, int8_t *out, float *scales, int64_t rows,
                             int64_t dim);
 int sglq_dequant_row_i8_host(const int8_t *q, float scale, float *out, int64_t n);
-int sglq_matmul_nt_host(const float *A, const float *W, const float *bias, float *C, int64_t M,
-                        int64_t N, int64_t K);
+/* f32 NT matmul with host A / bias / C and a device-resident W (from sglq_upload). */
+int sglq_matmul_nt_dev_w(const float *A, const float *dW, const float *bias, float *C,
+                         int64_t M, int64_t N, int64_t K, int dev);
+/* plain device copies of host buffers (the host layer's weight cache) */
+void *sglq_upload(const void *host, size_t bytes, int dev);
+void sglq_release(void *dptr, int dev);
 
 /* MoE: routed expert FFN over device-resident experts (see sgl_qmoe_forward). */
 int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down, int n_exp, const void *h,

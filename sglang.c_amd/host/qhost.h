@@ -35,4 +35,7 @@ int qj_bool(const qj *obj, const char *key, int def);
 int qh_plan_groups(sglq_plan *p, int64_t ngroups, const int32_t *gidx, int spc,
                    int32_t **kmap, int32_t **kinv);
 
+/* W8 weight (sgl_matmul_w8a16 operands) into the device layout; NULL after logging on error */
+sglq_dev *qh_build_w8(const int8_t *W, const float *sw, int64_t N, int64_t K, int dev);
+
 #endif

@@ -368,7 +368,7 @@ static sglq_dev *build_mxfp4(const uint8_t *wpacked, int64_t rows, int64_t cols,
   return d;
 }
 
-static sglq_dev *build_w8(const int8_t *W, const float *sw, int64_t N, int64_t K, int dev) {
+sglq_dev *qh_build_w8(const int8_t *W, const float *sw, int64_t N, int64_t K, int dev) {
   if (!W || !sw || N <= 0 || K <= 0) return NULL;
   if (!EXTENTS_OK("w8", N, K)) return NULL;
   sglq_plan p;
@@ -486,7 +486,7 @@ QH_API sgl_qlinear *sgl_qlinear_create_mxfp4(const uint8_t *wpacked, int64_t row
 
 QH_API sgl_qlinear *sgl_qlinear_create_w8(const int8_t *W, const float *sw, int64_t N, int64_t K,
                                           int dev) {
-  return wrap(build_w8(W, sw, N, K, dev));
+  return wrap(qh_build_w8(W, sw, N, K, dev));
 }
 
 QH_API int sgl_qlinear_forward(sgl_qlinear *ql, const void *A, int a_dtype, int64_t M,

@@ -24,7 +24,9 @@ int64_t sglq_N(const sglq_dev *d) { (void)d; return 0; }
 int64_t sglq_K(const sglq_dev *d) { (void)d; return 0; }
 int sglq_quant_rows_i8_host(const float *x, int8_t *o, float *s, int64_t r, int64_t d) { (void)x; (void)o; (void)s; (void)r; (void)d; return -1; }
 int sglq_dequant_row_i8_host(const int8_t *q, float s, float *o, int64_t n) { (void)q; (void)s; (void)o; (void)n; return -1; }
-int sglq_matmul_nt_host(const float *a, const float *w, const float *b, float *c, int64_t m, int64_t n, int64_t k) { (void)a; (void)w; (void)b; (void)c; (void)m; (void)n; (void)k; return -1; }
+int sglq_matmul_nt_dev_w(const float *a, const float *w, const float *b, float *c, int64_t m, int64_t n, int64_t k, int dev) { (void)a; (void)w; (void)b; (void)c; (void)m; (void)n; (void)k; (void)dev; return -1; }
+void *sglq_upload(const void *h, size_t n, int dev) { (void)h; (void)n; (void)dev; return NULL; }
+void sglq_release(void *p, int dev) { (void)p; (void)dev; }
 int sglq_moe_forward(sglq_dev *const *g, sglq_dev *const *d, int n, const void *h, int t, int64_t T, const int32_t *i, const float *w, int k, float *o, void *s) { (void)g; (void)d; (void)n; (void)h; (void)t; (void)T; (void)i; (void)w; (void)k; (void)o; (void)s; return -1; }
 int sglq_moe_router_logits(const float *r, int n, const void *h, int t, int64_t T, int64_t E, float *l, void *s) { (void)r; (void)n; (void)h; (void)t; (void)T; (void)E; (void)l; (void)s; return -1; }
 int sglq_moe_route(const float *l, int64_t T, int n, const float *b, int sg, int ng, int tg, int k, int nm, float sc, int32_t *i, float *w, void *s) { (void)l; (void)T; (void)n; (void)b; (void)sg; (void)ng; (void)tg; (void)k; (void)nm; (void)sc; (void)i; (void)w; (void)s; return -1; }

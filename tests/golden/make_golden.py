@@ -18,6 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "sglang.c_amd"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
 from oracle.oracle import Reference, make_cfg  # noqa: E402
 import synth  # noqa: E402
 

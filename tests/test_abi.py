@@ -12,7 +12,7 @@ import pytest
 from conftest import ROOT, golden
 
 LIB = os.path.join(ROOT, "sglang.c_amd", "libsgl_qlinear.so")
-HEADERS = ["qweight.h", "quant.h", "ops.h", "qlinear.h", "qload.h"]
+HEADERS = ["qweight.h", "quant.h", "ops.h", "qlinear.h", "qload.h", "qcache.h"]
 
 
 def declared_functions():
