@@ -74,6 +74,17 @@ sgl_qlinear *sgl_qlinear_create_w8(const int8_t *W, const float *sw, int64_t N, 
 int sgl_qlinear_forward(sgl_qlinear *ql, const void *A, int a_dtype, int64_t M,
                         const float *bias, float *C, void *stream);
 
+/* sgl_qlinear_forward that allocates nothing.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
+ * sgl_qlinear_forward; the prefill GEMM (M > 32 rows of f32, M > 24 of 16-bit activations)
+ * takes its workspace from a 64 MiB array the library holds on every GPU it runs on, and
+ * returns -1 (after a log line) when M rows need more than that (e.g. K = 4096: about 4000
+ * f32 rows, 8000 16-bit rows).  All calls on one GPU share that array: calls that can overlap
+ * on one GPU (two streams, two threads) race, so order them. */
+int sgl_qlinear_forward_noalloc(sgl_qlinear *ql, const void *A, int a_dtype, int64_t M,
+                                const float *bias, float *C, void *stream);
+
 /* W as f32 [N,K] into device memory: bit-identical to the reference dequant of the inputs. */
 int sgl_qlinear_dequant(sgl_qlinear *ql, float *out, void *stream);
 

@@ -1551,25 +1551,46 @@ fail:
   return -1;
 }
 
-int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
-              float *C, int64_t ldc, hipStream_t st) {
+// Workspace of a prefill GEMM of M rows: A operands, row exponents, split-K partials.
+static void gemm_ws_layout(const sglq_dev *d, int dt, int64_t M, int64_t *Mpad_out,
+                           size_t *aop_bytes, size_t *o_part, size_t *part_bytes) {
   const int split = dt == SGLQ_DT_F32;
-  const int64_t bmr = sglq_gemm_rows(d, split);
   // rows of A operands: whole row tiles of the LDS kernel's tiling (it reads no further), else
   // whole 128- and 256-row blocks
   const int64_t rt = lds_direct(d) ? lds_rows(lds_plan(d, M).cfg) : 256;
   const int64_t Mpad = (M + rt - 1) / rt * rt;
-  const size_t aop_bytes = sglq_aop_bytes(d, Mpad, split);
-  const size_t o_part = (aop_bytes + (size_t)Mpad * sizeof(int) + 255) / 256 * 256;
-  const size_t part_bytes =
-      lds_direct(d) ? (size_t)lds_plan(d, M).nz * M * d->N * sizeof(float) : 0;
-  if (sglq_ws_reserve(d, o_part + part_bytes + 256) != 0) return -1;
-  void *aop = d->ws;
-  int *rowexp = (int *)((char *)d->ws + aop_bytes);
-  float *part = part_bytes > (size_t)M * d->N * sizeof(float) ? (float *)((char *)d->ws + o_part)
+  *Mpad_out = Mpad;
+  *aop_bytes = sglq_aop_bytes(d, Mpad, split);
+  *o_part = (*aop_bytes + (size_t)Mpad * sizeof(int) + 255) / 256 * 256;
+  *part_bytes = lds_direct(d) ? (size_t)lds_plan(d, M).nz * M * d->N * sizeof(float) : 0;
+}
+
+size_t sglq_gemm_ws_bytes(const sglq_dev *d, int dt, int64_t M) {
+  int64_t Mpad;
+  size_t aop_bytes, o_part, part_bytes;
+  gemm_ws_layout(d, dt, M, &Mpad, &aop_bytes, &o_part, &part_bytes);
+  return o_part + part_bytes + 256;
+}
+
+int sglq_gemm_ws(const sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M,
+                 const float *bias, float *C, int64_t ldc, void *ws, hipStream_t st) {
+  const int split = dt == SGLQ_DT_F32;
+  const int64_t bmr = sglq_gemm_rows(d, split);
+  int64_t Mpad;
+  size_t aop_bytes, o_part, part_bytes;
+  gemm_ws_layout(d, dt, M, &Mpad, &aop_bytes, &o_part, &part_bytes);
+  void *aop = ws;
+  int *rowexp = (int *)((char *)ws + aop_bytes);
+  float *part = part_bytes > (size_t)M * d->N * sizeof(float) ? (float *)((char *)ws + o_part)
                                                               : nullptr;
   if (sglq_prep_a(d, 0, A, dt, lda, M, Mpad, nullptr, 0, split, aop, rowexp, st) != 0)
     return -1;
   return sglq_gemm_run(d, nullptr, aop, rowexp, M, Mpad, (Mpad + bmr - 1) / bmr, split, bias, C,
                        ldc, part, st);
+}
+
+int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
+              float *C, int64_t ldc, hipStream_t st) {
+  if (sglq_ws_reserve(d, sglq_gemm_ws_bytes(d, dt, M)) != 0) return -1;
+  return sglq_gemm_ws(d, A, dt, lda, M, bias, C, ldc, d->ws, st);
 }

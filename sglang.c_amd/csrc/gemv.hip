@@ -1178,8 +1178,11 @@ int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows
   return launch_gemv(d, a, pl, split, amode != 2 && aligned, (unsigned)max_segs, st);
 }
 
-extern "C" int sglq_forward(sglq_dev *d, const void *A, int dt, int64_t M, const float *bias,
-                            float *C, void *stream) {
+// C = A W^T (+ bias): decode GEMV up to 16 rows (and 17-32 rows as two GEMVs), prefill GEMM
+// beyond.  ws == nullptr: the GEMM uses the handle's workspace (grown on first use at a size);
+// otherwise ws (ws_bytes, 256-byte aligned) is the GEMM workspace and nothing is allocated.
+int sglq_forward_ws(sglq_dev *d, const void *A, int dt, int64_t M, const float *bias, float *C,
+                    void *stream, void *ws, size_t ws_bytes) {
   hipStream_t st = (hipStream_t)stream;
   const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
   SGLQ_HIP(hipSetDevice(d->dev));
@@ -1196,9 +1199,23 @@ extern "C" int sglq_forward(sglq_dev *d, const void *A, int dt, int64_t M, const
     return sglq_gemv(d, (const char *)A + 16 * d->K * esz, dt, d->K, M - 16, bias,
                      C + 16 * d->N, d->N, st);
   }
-  if (M > 16) return sglq_gemm(d, A, dt, d->K, M, bias, C, d->N, st);
+  if (M > 16) {
+    if (!ws) return sglq_gemm(d, A, dt, d->K, M, bias, C, d->N, st);
+    const size_t need = sglq_gemm_ws_bytes(d, dt, M);
+    if (need > ws_bytes) {
+      sglq_log_error("qlinear: %lld rows need %zu bytes of workspace, %zu available",
+                     (long long)M, need, ws_bytes);
+      return -1;
+    }
+    return sglq_gemm_ws(d, A, dt, d->K, M, bias, C, d->N, ws, st);
+  }
   return sglq_gemv(d, A, dt, d->K, M, bias, C, d->N, st);
 fail:
   return -1;
+}
+
+extern "C" int sglq_forward(sglq_dev *d, const void *A, int dt, int64_t M, const float *bias,
+                            float *C, void *stream) {
+  return sglq_forward_ws(d, A, dt, M, bias, C, stream, nullptr, 0);
 }
 

@@ -112,9 +112,17 @@ int sglq_launch_dequant_row_i8(const int8_t *q, float scale, float *o, int64_t n
                                hipStream_t st);
 int sglq_launch_matmul_nt(const float *A, const float *W, const float *bias, float *C,
                           int64_t M, int64_t N, int64_t K, hipStream_t st);
+// Forward on an optional caller workspace for the prefill GEMM (gemv.hip; see there).
+int sglq_forward_ws(sglq_dev *d, const void *A, int dt, int64_t M, const float *bias, float *C,
+                    void *stream, void *ws, size_t ws_bytes);
 // Prefill GEMM launch (gemm.hip): any M; grows the handle's workspace on first use at a size.
 int sglq_gemm(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const float *bias,
               float *C, int64_t ldc, hipStream_t st);
+// The same GEMM on a caller-provided workspace of at least sglq_gemm_ws_bytes bytes
+// (256-byte aligned); allocates nothing.
+size_t sglq_gemm_ws_bytes(const sglq_dev *d, int dt, int64_t M);
+int sglq_gemm_ws(const sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M,
+                 const float *bias, float *C, int64_t ldc, void *ws, hipStream_t st);
 
 // Grouped-GEMM building blocks (gemm.hip), used by the MoE path.
 constexpr int SGLQ_GEMM_BM = 128;  // rows per GEMM row block

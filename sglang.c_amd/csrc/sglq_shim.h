@@ -71,6 +71,11 @@ int sglq_dequant_host(sglq_dev *d, float *out_host);
 /* C[M,N] = A[M,K] * W^T (+ bias), A in a_dtype, everything in device memory. */
 int sglq_forward(sglq_dev *d, const void *A, int a_dtype, int64_t M, const float *bias,
                  float *C, void *stream);
+/* Same as sglq_forward with the prefill GEMM's workspace in the library's per-device scratch
+ * array (noalloc.hip): allocates nothing; -1 if M rows need more than sglq_scratch_bytes(). */
+int sglq_forward_noalloc(sglq_dev *d, const void *A, int a_dtype, int64_t M, const float *bias,
+                         float *C, void *stream);
+size_t sglq_scratch_bytes(void);
 /* Host-pointer convenience (synchronous): uploads A/bias, downloads C. */
 int sglq_forward_host(sglq_dev *d, const float *A, int64_t M, const float *bias, float *C);
 

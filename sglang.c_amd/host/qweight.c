@@ -501,6 +501,18 @@ QH_API int sgl_qlinear_forward(sgl_qlinear *ql, const void *A, int a_dtype, int6
   return sglq_forward(ql->d, A, a_dtype, M, bias, C, stream);
 }
 
+QH_API int sgl_qlinear_forward_noalloc(sgl_qlinear *ql, const void *A, int a_dtype, int64_t M,
+                                       const float *bias, float *C, void *stream) {
+  if (!ql || M < 0) return -1;
+  if (a_dtype != SGL_QL_F32 && a_dtype != SGL_QL_BF16 && a_dtype != SGL_QL_F16) {
+    QH_ERR("qlinear: unknown activation dtype %d", a_dtype);
+    return -1;
+  }
+  if (M == 0) return 0;
+  if (!A || !C) return -1;
+  return sglq_forward_noalloc(ql->d, A, a_dtype, M, bias, C, stream);
+}
+
 QH_API int sgl_qlinear_dequant(sgl_qlinear *ql, float *out, void *stream) {
   if (!ql || !out) return -1;
   return sglq_dequant_dev(ql->d, out, stream);

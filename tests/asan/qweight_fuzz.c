@@ -17,6 +17,7 @@ sglq_dev *sglq_build(const sglq_plan *p, const void *w, const void *z, const voi
 int sglq_dequant_dev(sglq_dev *d, float *o, void *s) { (void)d; (void)o; (void)s; return -1; }
 int sglq_dequant_host(sglq_dev *d, float *o) { (void)d; (void)o; return -1; }
 int sglq_forward(sglq_dev *d, const void *a, int t, int64_t m, const float *b, float *c, void *s) { (void)d; (void)a; (void)t; (void)m; (void)b; (void)c; (void)s; return -1; }
+int sglq_forward_noalloc(sglq_dev *d, const void *a, int t, int64_t m, const float *b, float *c, void *s) { (void)d; (void)a; (void)t; (void)m; (void)b; (void)c; (void)s; return -1; }
 int sglq_forward_host(sglq_dev *d, const float *a, int64_t m, const float *b, float *c) { (void)d; (void)a; (void)m; (void)b; (void)c; return -1; }
 void sglq_free(sglq_dev *d) { (void)d; }
 int64_t sglq_weight_bytes(const sglq_dev *d) { (void)d; return 0; }
