@@ -206,6 +206,7 @@ def extra_configs(torch, q, warmup, only=EXTRA_SECTIONS):
         q8, s8 = synth.quant_rows_i8(W)
         gemv_line(torch, q, lambda c: [q.QLinear.from_w8(q8, s8) for _ in range(c)],
                   4864 * 896 + 4864 * 4, [1, 8], torch.float32, warmup, "w8_4864x896_f32", out)
+        out["w8_hostptr_4864x896_f32_M1"] = hostptr_w8_line(q, q8, s8)
     # config 4: MXFP4 [8192, 8192], M = 1 and 16 (GEMV), 512 (GEMM), bf16
     if "mxfp4" in only:
         Wm = synth.normal(0x5EED0004, (8192, 8192), 0.02)
@@ -281,6 +282,35 @@ def ceilings(torch, warmup):
             "frac_f16_mfma_peak": round(fl / t / 1e12 / F16_PEAK_TFLOPS, 4),
             "us": round(t * 1e6, 1)}
     return res
+
+
+def hostptr_w8_line(q, q8, s8, calls=200):
+    """The unchanged-caller drop-in: sgl_matmul_w8a16 on host buffers, M = 1 (reference
+    src/llama.c:876-884 calls it per projection).  The weight is resident after the first call;
+    each call copies the row in and the result out and synchronises.  Wall clock per call,
+    median; beside it the reference's own CPU function on the same operands (oracle/_ref, or
+    the oracle restatement), single-threaded at M = 1 by construction (reference
+    src/quant.c:46)."""
+    import synth
+    from oracle.oracle import Oracle, Reference, have_reference
+    A = synth.normal(0x5EED0110, (1, 896))
+    q.matmul_w8a16(A, q8, s8)  # first call uploads the weight
+    ts = []
+    for _ in range(calls):
+        t0 = time.perf_counter()
+        q.matmul_w8a16(A, q8, s8)
+        ts.append(time.perf_counter() - t0)
+    ref = Reference() if have_reference() else Oracle()
+    cs = []
+    for _ in range(max(20, calls // 4)):
+        t0 = time.perf_counter()
+        ref.matmul_w8a16(A, q8, s8)
+        cs.append(time.perf_counter() - t0)
+    wb = 4864 * 896 + 4864 * 4
+    return {"us_per_call": round(median(ts) * 1e6, 1), "GB/s": round(wb / median(ts) / 1e9, 1),
+            "cpu_us_per_call": round(median(cs) * 1e6, 1),
+            "cpu_kind": "reference" if have_reference() else "port",
+            "note": "host buffers in and out, synchronous, PCIe-inclusive"}
 
 
 def gemm_configs(torch, q, warmup, out):
