@@ -270,6 +270,15 @@ def ceilings(torch, warmup):
         res[tag] = {"TFLOP/s": round(flops / t / 1e12, 1),
                     "frac_f16_mfma_peak": round(flops / t / 1e12 / F16_PEAK_TFLOPS, 4),
                     "us": round(t * 1e6, 1)}
+    lib.sglc_lds_read.argtypes = [C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    for per_cu in (1, 2, 4):
+        grid, iters = 256 * per_cu, 4096
+        t = time_graph(torch, lambda: lib.sglc_lds_read(grid, iters, C.c_void_p(sink.data_ptr()),
+                                                        st()), REPLAYS, warmup)
+        nbytes = grid * 256 * iters * 128
+        res[f"lds_read_b128_{per_cu}wg_per_cu"] = {
+            "TB/s": round(nbytes / t / 1e12, 2),
+            "bytes_per_cu_per_ns": round(nbytes / t / 1e9 / 256, 1), "us": round(t * 1e6, 1)}
     import synth
     for M in (512, 2048):
         A = torch.from_numpy(synth.normal(0x5EED0105, (M, 4096))).cuda().half()

@@ -140,6 +140,24 @@ __global__ __launch_bounds__(256) void k_mfma_32x32x16_f16(int iters, float *__r
   if (s == 1234.5678f) sink[threadIdx.x] = s;
 }
 
+// LDS read stream: every lane reads 16 B per ds_read_b128 from a 64 KiB LDS array, eight reads
+// in flight, consecutive lanes on consecutive 16-byte slots (no bank conflicts).
+__global__ __launch_bounds__(256) void k_lds_read(int iters, int stride, uint32_t *__restrict__ sink) {
+  __shared__ u4_t buf[4096];  // 64 KiB
+  for (int i = threadIdx.x; i < 4096; i += 256) buf[i] = u4_t{(uint32_t)i, 1u, 2u, 3u};
+  __syncthreads();
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  u4_t x = {0, 0, 0, 0};
+  for (int it = 0; it < iters; it++) {
+    u4_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = buf[(it * stride + j * 256 + w * 64 + lane) & 4095];
+#pragma unroll
+    for (int j = 0; j < 8; j++) x += v[j];
+  }
+  if ((x.x ^ x.y ^ x.z ^ x.w) == 0x9E3779B9u) sink[threadIdx.x] = x.x;
+}
+
 extern "C" {
 
 // bytes read = n16 * 16; u = loads in flight per thread (4 / 8 / 16)
@@ -173,6 +191,14 @@ __attribute__((visibility("default"))) int sglc_mfma(int kind, int grid, int ite
     k_mfma_32x32x16_f16<<<grid, 256, 0, st>>>(iters, sink);
   else
     k_mfma_16x16x32_f16_builtin<<<grid, 256, 0, st>>>(iters, sink);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// LDS read stream on `grid` workgroups of 256 threads: bytes read = grid * 256 * iters * 128.
+__attribute__((visibility("default"))) int sglc_lds_read(int grid, int iters, uint32_t *sink,
+                                                          void *stream) {
+  // the stride (a multiple of 64 items, unknown to the compiler) keeps every read in the loop
+  k_lds_read<<<grid, 256, 0, (hipStream_t)stream>>>(iters, 8 * 256 + 64, sink);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
