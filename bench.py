@@ -483,7 +483,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
-                     "kernel": "k_gemv_wave (one-row decode GEMV), int4 GPTQ g128",
+                     "kernel": "k_gemv_row (one-row decode GEMV), int4 GPTQ g128",
                      "algorithmic_bytes_per_launch": launch_bytes,
                      "us_per_launch": {"11008x4096": round(t_gate * 1e6, 2),
                                        "4096x11008": round(t_down * 1e6, 2)}},
