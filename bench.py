@@ -279,6 +279,33 @@ def ceilings(torch, warmup):
         res[f"lds_read_b128_{per_cu}wg_per_cu"] = {
             "TB/s": round(nbytes / t / 1e12, 2),
             "bytes_per_cu_per_ns": round(nbytes / t / 1e9 / 256, 1), "us": round(t * 1e6, 1)}
+    # VALU work beside MFMAs: ns per MFMA per SIMD with nv independent v_pk_mul_f16 after each
+    # MFMA, at 1, 2 and 4 waves per SIMD (256 / 512 / 1024 workgroups of 4 waves)
+    lib.sglc_mfma_valu.argtypes = [C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p]
+    for g in (256, 512, 1024):
+        for nv in (0, 2, 4):
+            iters = 2000
+            t = time_graph(torch, lambda: lib.sglc_mfma_valu(nv, g, iters,
+                                                             C.c_void_p(sink.data_ptr()), st()),
+                           REPLAYS, warmup)
+            res[f"mfma_valu_{g // 256}w_per_simd_nv{nv}"] = {
+                "ns_per_mfma_per_simd": round(t * 1e9 / (iters * 8 * g / 256), 3)}
+    # one CU's intake of data that hits in L2 (64 KiB per workgroup, 2 MiB per XCD) or misses
+    # it (256 KiB per workgroup), one workgroup per CU, 8 and 16 loads in flight per thread
+    lib.sglc_l2_read.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                 C.c_void_p]
+    for kb in (64, 256):
+        slice16 = kb * 1024 // 16
+        buf = torch.ones(256 * slice16 * 4, dtype=torch.int32, device="cuda")
+        iters = max(1, (64 << 20) // (256 * slice16 * 16)) * 4
+        for u in (8, 16):
+            t = time_graph(torch, lambda: lib.sglc_l2_read(
+                C.c_void_p(buf.data_ptr()), 256, slice16, iters, u,
+                C.c_void_p(sink.data_ptr()), st()), REPLAYS, warmup)
+            nb = 256 * slice16 * 16 * iters
+            res[f"cu_read_{kb}KiB_per_cu_u{u}"] = {"TB/s": round(nb / t / 1e12, 2),
+                                                    "GB/s_per_cu": round(nb / t / 1e9 / 256, 1)}
+        del buf
     import synth
     for M in (512, 2048):
         A = torch.from_numpy(synth.normal(0x5EED0105, (M, 4096))).cuda().half()

@@ -30,6 +30,27 @@ __global__ __launch_bounds__(256) void k_stream_read(const u4_t *__restrict__ p,
   if (x == 0x9E3779B9u) sink[blockIdx.x & 1023] = x;
 }
 
+// L2-resident read stream: workgroup b reads its own slice of `slice16` 16-byte items `iters`
+// times (plain loads, U per thread in flight per pass).  Slices small enough for the L2 of the
+// workgroup's XCD measure how fast one CU takes in data that hits in L2.
+template <int U>
+__global__ __launch_bounds__(256) void k_l2_read(const u4_t *__restrict__ p, int slice16, int iters,
+                                                 uint32_t *__restrict__ sink) {
+  const u4_t *q = p + (int64_t)blockIdx.x * slice16;
+  uint32_t x = 0;
+  for (int it = 0; it < iters; it++) {
+    for (int b = 0; b < slice16; b += 256 * U) {
+      u4_t v[U];
+#pragma unroll
+      for (int u = 0; u < U; u++) v[u] = q[(b + u * 256 + threadIdx.x) % slice16];
+#pragma unroll
+      for (int u = 0; u < U; u++) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    x = x * 3u + (uint32_t)it;
+  }
+  if (x == 0x9E3779B9u) sink[blockIdx.x & 1023] = x;
+}
+
 __global__ void k_empty() {}
 
 // MFMA issue loops: every wave runs `iters` x 8 independent accumulation chains.  Operands come
@@ -142,6 +163,45 @@ __global__ __launch_bounds__(256) void k_mfma_32x32x16_f16(int iters, float *__r
 
 // LDS read stream: every lane reads 16 B per ds_read_b128 from a 64 KiB LDS array, eight reads
 // in flight, consecutive lanes on consecutive 16-byte slots (no bank conflicts).
+// MFMA issue with independent VALU work: every wave runs `iters` x 8 independent accumulation
+// chains of v_mfma_f32_16x16x32_f16, each instruction followed by NV v_pk_mul_f16 on registers
+// no MFMA touches.  Run at one and two waves per SIMD, it shows whether the SIMD issues VALU
+// work in the shadow of its own wave's MFMAs or only of another wave's.
+template <int NV>
+__global__ __launch_bounds__(256) void k_mfma_valu(int iters, float *__restrict__ sink) {
+  h8_t a, b;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    a[i] = (_Float16)(0.001f * (threadIdx.x + i));
+    b[i] = (_Float16)(0.002f * (threadIdx.x - i));
+  }
+  const float z = (float)threadIdx.x;
+  f4_t c[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) c[i] = (f4_t){z + i, 0, 0, 0};
+  uint32_t v[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) v[i] = 0x3c003c00u + threadIdx.x + i;
+  const uint32_t m = 0x3c013c01u;
+  for (int it = 0; it < iters; it++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(c[i]) : "v"(a), "v"(b));
+#pragma unroll
+      for (int u = 0; u < NV; u++)
+        asm volatile("v_pk_mul_f16 %0, %0, %1" : "+v"(v[(i * NV + u) & 7]) : "v"(m));
+    }
+  }
+  f4_t t = c[0];
+#pragma unroll
+  for (int i = 1; i < 8; i++) t += c[i];
+  uint32_t x = 0;
+#pragma unroll
+  for (int i = 0; i < 8; i++) x ^= v[i];
+  const float s = (t[0] + t[1]) + (t[2] + t[3]) + (float)x;
+  if (s == 1234.5678f) sink[threadIdx.x] = s;
+}
+
 __global__ __launch_bounds__(256) void k_lds_read(int iters, int stride, uint32_t *__restrict__ sink) {
   __shared__ u4_t buf[4096];  // 64 KiB
   for (int i = threadIdx.x; i < 4096; i += 256) buf[i] = u4_t{(uint32_t)i, 1u, 2u, 3u};
@@ -199,6 +259,29 @@ __attribute__((visibility("default"))) int sglc_lds_read(int grid, int iters, ui
                                                           void *stream) {
   // the stride (a multiple of 64 items, unknown to the compiler) keeps every read in the loop
   k_lds_read<<<grid, 256, 0, (hipStream_t)stream>>>(iters, 8 * 256 + 64, sink);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// MFMA + VALU issue (k_mfma_valu): nv VALU per MFMA (0, 2, 4 or 6) on `grid` workgroups of 256.
+__attribute__((visibility("default"))) int sglc_mfma_valu(int nv, int grid, int iters, float *sink,
+                                                           void *stream) {
+  hipStream_t st = (hipStream_t)stream;
+  if (nv == 0) k_mfma_valu<0><<<grid, 256, 0, st>>>(iters, sink);
+  else if (nv == 2) k_mfma_valu<2><<<grid, 256, 0, st>>>(iters, sink);
+  else if (nv == 4) k_mfma_valu<4><<<grid, 256, 0, st>>>(iters, sink);
+  else k_mfma_valu<6><<<grid, 256, 0, st>>>(iters, sink);
+  return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// L2-resident read stream (k_l2_read): bytes read = grid * slice16 * 16 * iters.
+__attribute__((visibility("default"))) int sglc_l2_read(const void *p, int grid, int slice16,
+                                                         int iters, int u, uint32_t *sink,
+                                                         void *stream) {
+  hipStream_t st = (hipStream_t)stream;
+  if (u == 16)
+    k_l2_read<16><<<grid, 256, 0, st>>>((const u4_t *)p, slice16, iters, sink);
+  else
+    k_l2_read<8><<<grid, 256, 0, st>>>((const u4_t *)p, slice16, iters, sink);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -10,6 +10,9 @@
 //             into LDS next to the A operands, through a ring of LDS buffers, and its waves run
 //             v_mfma_f32_16x16x32_f16 from there.  Small M splits the stages over K, and
 //             k_splitk_reduce adds the slices in order.
+//   k_gemm_dma  the same weights, dense, where enough 128-row tiles exist (K <= 4096): wide
+//             tiles (192 or 384 columns), codes unpacked in registers once per workgroup,
+//             A operands copied global -> LDS through a four-deep ring.
 //   k_gemm_breg  the same weights in the grouped (MoE) launches, 64-row expert blocks: the A
 //             operands through LDS, each wave's codes unpacked in registers (one wave per
 //             weight tile there, so LDS would buy no reuse); same products as k_gemm_lds.
@@ -18,6 +21,7 @@
 // MXFP4 block scales are folded into the fp4 -> f16 conversion relative to a per-column
 // exponent (exact for every block within 2^23 of the column's largest), applied at the end.
 #include <stdlib.h>
+#include <stdio.h>
 #include <string.h>
 
 #include "sglq_dev.hpp"
@@ -1152,6 +1156,287 @@ __global__ __launch_bounds__(64 * WN, 2) void k_gemm_breg(GemmArgs a) {
   lds_epilogue<MB, TN, NT16, E2M1>(a, acc, m0, mend, bn, wn, colexp, n16, kq);
 }
 
+// Epilogue of the dense register-B kernels: the tile goes through LDS (16, 8 or 4 rows at a
+// time) so that consecutive threads store consecutive 16-byte pieces of whole rows of C (or of
+// the K-split partials), instead of each lane storing 4-byte values of four rows.  C[m][n] =
+// 2^(rowexp[m] + ce[n]) acc + bias[n]; partials are stored unscaled.  stg: at least
+// RP x 64 TN floats of LDS, free for this use (every wave is past its last LDS read).
+template <int MBW, int TN, bool E2M1, int RP, int WN>
+__device__ __forceinline__ void wide_epilogue(const GemmArgs &a, const float4_t (&acc)[MBW][TN],
+                                              float *stg, int m0, int bn, int w, int n16,
+                                              int kq) {
+  // wave w holds every 16-row block i < MBW of column group w; pass (i, h) stages rows
+  // h RP .. h RP + RP - 1 of block i
+  constexpr int COLS = 16 * WN * TN, C4 = COLS / 4, ITEMS = RP * C4, NTH = 64 * WN;
+  const int tid = threadIdx.x;
+  const int nb = bn * COLS;
+  float *out = a.part ? a.part + (int64_t)blockIdx.y * a.M * a.N : a.C;
+  const int64_t ld = a.part ? a.N : a.ldc;
+  const bool vec = ((uintptr_t)out % 16 == 0) && (ld % 4 == 0) && (a.N % 4 == 0);
+#pragma unroll
+  for (int i = 0; i < MBW; i++) {
+#pragma unroll
+    for (int h = 0; h < 16 / RP; h++) {
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int row = 4 * kq + r - h * RP;
+          if (row >= 0 && row < RP)
+            stg[row * COLS + (w * TN + j) * 16 + n16] = acc[i][j][r];
+        }
+      __syncthreads();
+      for (int e = tid; e < ITEMS; e += NTH) {
+        const int row = e / C4, c4 = e % C4;
+        const int m = m0 + 16 * i + h * RP + row, n = nb + 4 * c4;
+        if (m >= a.M || n >= a.N) continue;
+        float4_t v = *(const float4_t *)(stg + row * COLS + 4 * c4);
+        if (!a.part) {
+          const int re = a.rowexp[m];
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            const int nn = min(n + u, a.N - 1);
+            const int ce = E2M1 ? (int)a.colexp[nn] - 127 : 0;
+            v[u] = ldexpf(v[u], re + ce) + (a.bias ? a.bias[nn] : 0.f);
+          }
+        }
+        float *o = out + (int64_t)m * ld + n;
+        if (vec) {
+          *(float4_t *)o = v;
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; u++)
+            if (n + u < a.N) o[u] = v[u];
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Tile of k_gemm_dma's workgroup.  Workgroups go round-robin over the 8 XCDs
+// (blockIdx.x & 7); each XCD takes a contiguous run of tiles in row-block-major order, so it
+// holds few row blocks and its L2 keeps their A rows.  (Column-block-major order, where each
+// XCD reads its weights once, and row-block pairs measured the same at M = 512 and 2048.)
+__device__ __forceinline__ bool wide_tile(const GemmArgs &a, int &bm, int &bn) {
+  const int total = a.nbm * a.nbn, per = (total + 7) >> 3;
+  const int idx = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (idx >= total) return false;
+  bm = idx / a.nbn;
+  bn = idx % a.nbn;
+  return true;
+}
+
+// s_waitcnt that waits until at most n vector memory operations of this wave are outstanding
+// (expcnt and lgkmcnt left alone): gfx9 encoding, vmcnt in bits 3:0 and 15:14
+#define SGLQ_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | 0x70 | 0xF00)
+
+// Dense prefill GEMM on the direct formats, deep asynchronous pipeline.  A workgroup of WN
+// waves covers 16 MB rows x 16 WN TN columns; wave w owns weight tiles WN TN bn + TN w + j
+// (j < TN) over all rows, so each code is loaded and unpacked once per workgroup, in
+// registers, and only the A operands go through LDS:
+//   * A operands go global -> LDS directly (global_load_lds_dwordx4, no registers) into a
+//     ring of four buffers, issued three chunks ahead of their use;
+//   * codes and meta of a chunk are loaded into a 4-deep register ring four chunks ahead;
+//   * the loop body is four chunks, so every buffer and register set is named statically;
+//     chunks past the end compute with zero scales (adding exact zeros);
+//   * one barrier per chunk, after this wave's own copies of the chunk have landed (an
+//     explicit vmcnt wait: the copies of the next chunks stay in flight);
+//   * VALU work does not issue in the shadow of the same wave's MFMAs on gfx950 (measured with
+//     k_mfma_valu), so the unpack is kept to one pass per workgroup, and with 4 waves (one per
+//     SIMD) the A fragments of a chunk are read up front and the unpack of step s + 1 is
+//     interleaved with step s's MFMAs (SCHED); 8 waves (two per SIMD) overlap each other.
+// Products are those of k_gemm_lds (same prescale and unpack); the epilogue stores whole rows.
+template <int KIND, int NP, int TN, int MB, bool SCHED, int WN>
+__global__ __launch_bounds__(64 * WN, 1) void k_gemm_dma(GemmArgs a) {
+  constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
+  constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
+  constexpr int BMR = 16 * MB;
+  constexpr int NT16 = WN * TN;
+  constexpr int SLOTS = NP * SPC * 4;  // 16-B A slots (piece, step, kq) per chunk
+  constexpr int AITEMS = SLOTS * BMR;  // 16-B A items per chunk
+  constexpr int NTH = 64 * WN;       // WN waves along N
+  constexpr int MBW = MB;            // 16-row blocks per wave (all rows of the tile)
+  constexpr int AIPT = AITEMS / NTH;  // copies per thread per chunk
+  constexpr int RPI = NTH / BMR;
+  static_assert(AITEMS % NTH == 0 && NTH % BMR == 0, "k_gemm_dma: row tile");
+  // four separately declared buffers: the compiler then tells the copies into one buffer from
+  // reads of another and does not wait for every outstanding copy before an LDS read
+  __shared__ half8_t sA0[AITEMS], sA1[AITEMS], sA2[AITEMS], sA3[AITEMS];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = tid >> 6;  // column group
+  const int n16 = lane & 15, kq = lane >> 4;
+  int bm, bn;
+  if (!wide_tile(a, bm, bn)) return;
+  const int m0 = bm * BMR, mend = a.M;
+  const int c0 = (int)((int64_t)a.nchunk * blockIdx.y / gridDim.y);
+  const int c1 = (int)((int64_t)a.nchunk * (blockIdx.y + 1) / gridDim.y);
+
+  // copy q of this thread: LDS item tid + 256 q = row tid % BMR of slot RPI q + tid / BMR; the
+  // 64 lanes of a wave fill 1 KiB of LDS from 1 KiB of consecutive rows
+  const int64_t plane = (int64_t)a.nsteps * 4 * a.Mpad;
+  const half8_t *abase = a.aop + m0 + (tid % BMR) + (int64_t)(tid / BMR) * a.Mpad;
+  auto copy_a = [&](int c, half8_t *buf) {
+    const int cc = min(c, c1 - 1);
+#pragma unroll
+    for (int q = 0; q < AIPT; q++) {
+      const int r = RPI * q, p = r / (SPC * 4), sj = r % (SPC * 4);
+      const half8_t *g = abase + p * plane + ((int64_t)cc * SPC * 4 + sj) * a.Mpad;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)g,
+                                       (__attribute__((address_space(3))) void *)(buf + NTH * q + 64 * (tid >> 6)),
+                                       16, 0, 0);
+    }
+  };
+
+  const u32x4_t *bsrc[TN];
+  const uint32_t *msrc[TN];
+  int cref[TN];
+#pragma unroll
+  for (int j = 0; j < TN; j++) {
+    const int t = min(bn * NT16 + w * TN + j, a.ntile - 1);
+    bsrc[j] = a.codes + (int64_t)t * a.nchunk * 64 + lane;
+    msrc[j] = (const uint32_t *)a.meta + sglq_mrow(t, n16, E2M1 ? a.nmeta / 4 : a.nmeta);
+    cref[j] = 0;
+    if constexpr (E2M1) cref[j] = a.colexp[t * 16 + n16];
+  }
+  struct BSet {
+    u32x4_t code[TN];
+    uint32_t meta[TN];
+    bool live;
+  };
+  // chunks past the end reload the last chunk and compute with scale 0 (exact zero weights);
+  // the flag is applied where the values are used, so no load is waited for early
+  auto load_b = [&](int c, BSet &b) {
+    b.live = c < c1;
+    const int cc = min(c, c1 - 1);
+    const int u = E2M1 ? cc : cc / a.cpg;
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      b.code[j] = ldg_nt(bsrc[j] + (int64_t)cc * 64);
+      b.meta[j] = ldg(msrc[j] + sglq_mofs(u));
+    }
+  };
+
+  float4_t acc[MBW][TN];
+#pragma unroll
+  for (int i = 0; i < MBW; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) acc[i][j] = (float4_t){0.f, 0.f, 0.f, 0.f};
+
+  // one chunk: every A fragment of the chunk is read from LDS first (one LDS wait per chunk),
+  // then step s's MFMAs run while step s + 1's weights are unpacked; sched_group_barrier
+  // interleaves them (one MFMA, then up to two VALU), so the unpack issues in the MFMA shadow
+  auto unpack = [&](const BSet &b, int s, const half2_t(&zA)[TN], const half2_t(&zB)[TN],
+                    const half2_t(&s2)[TN], half8_t(&bv)[TN]) {
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      float fsc = 1.f;
+      if constexpr (E2M1)
+        fsc = b.live ? e8m0_rel((b.meta[j] >> (8 * s)) & 255u, cref[j]) : 0.f;
+      H8 u;
+      u.v = unpack_b<KIND>(b.code[j], s, zA[j], zB[j], fsc);
+      if constexpr (!E2M1) {
+#pragma unroll
+        for (int hh = 0; hh < 4; hh++) u.h[hh] = u.h[hh] * s2[j];
+      }
+      bv[j] = u.v;
+    }
+  };
+  auto compute = [&](const half8_t *buf, const BSet &b) {
+    half2_t zA[TN], zB[TN], s2[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      zA[j] = zB[j] = s2[j] = (half2_t){0, 0};
+      if constexpr (!E2M1) {
+        float sc;
+        decode_meta<true>(b.meta[j], sc, zA[j], zB[j]);
+        const _Float16 hs = b.live ? (_Float16)sc : (_Float16)0.f;
+        s2[j] = (half2_t){hs, hs};
+      }
+    }
+    const half8_t *sa = buf + kq * BMR + n16;
+    // SCHED: every A fragment of the chunk up front; otherwise per step (fewer registers)
+    constexpr int AS = SCHED ? SPC : 1;
+    half8_t av[AS][NP][MBW];
+    auto read_a = [&](int s) {
+#pragma unroll
+      for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int i = 0; i < MBW; i++)
+          av[SCHED ? s : 0][p][i] = sa[(p * SPC + s) * 4 * BMR + i * 16];
+    };
+    if constexpr (SCHED) {
+#pragma unroll
+      for (int s = 0; s < SPC; s++) read_a(s);
+    }
+    half8_t bv0[TN], bv1[TN];
+    unpack(b, 0, zA, zB, s2, bv0);
+    if constexpr (SCHED) __builtin_amdgcn_sched_barrier(0);  // the LDS reads stay first
+#pragma unroll
+    for (int s = 0; s < SPC; s++) {
+      half8_t(&cur)[TN] = (s & 1) ? bv1 : bv0;
+      half8_t(&nxt)[TN] = (s & 1) ? bv0 : bv1;
+      if constexpr (!SCHED) read_a(s);
+      if (s + 1 < SPC) unpack(b, s + 1, zA, zB, s2, nxt);
+      const int sa_ = SCHED ? s : 0;
+#pragma unroll
+      for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int i = 0; i < MBW; i++)
+#pragma unroll
+          for (int j = 0; j < TN; j++)
+            acc[i][j] =
+                __builtin_amdgcn_mfma_f32_16x16x32_f16(av[sa_][p][i], cur[j], acc[i][j], 0, 0, 0);
+      if constexpr (SCHED) {
+#pragma unroll
+        for (int x = 0; x < NP * MBW * TN; x++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // then up to two VALU
+        }
+      }
+    }
+  };
+
+  // issue order per chunk k: [wait for own copies of k, barrier] copies of k + 3, codes of
+  // k + 4 (after chunk k's codes are consumed).  At the top of chunk k the operations issued
+  // after the copies of k are: codes k+1, copies k+1, codes k+2, copies k+2, codes k+3.
+  constexpr int AFTER = 2 * AIPT + 3 * 2 * TN;
+  static_assert(AFTER <= 63, "k_gemm_dma: vmcnt range");
+  BSet b0, b1, b2, b3;
+  load_b(c0, b0);
+  copy_a(c0, sA0);
+  load_b(c0 + 1, b1);
+  copy_a(c0 + 1, sA1);
+  load_b(c0 + 2, b2);
+  copy_a(c0 + 2, sA2);
+  load_b(c0 + 3, b3);
+  auto chunk = [&](int k, half8_t *cur, half8_t *nxt3, BSet &b) {
+    SGLQ_WAIT_VMCNT(AFTER);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    copy_a(k + 3, nxt3);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(cur, b);
+    __builtin_amdgcn_sched_barrier(0);
+    load_b(k + 4, b);
+  };
+  for (int k = c0; k < c1; k += 4) {
+    chunk(k, sA0, sA3, b0);
+    chunk(k + 1, sA1, sA0, b1);
+    chunk(k + 2, sA2, sA1, b2);
+    chunk(k + 3, sA3, sA2, b3);
+  }
+  SGLQ_WAIT_VMCNT(0);  // no copy may land in LDS after the workgroup ends
+  (void)mend;
+  __syncthreads();
+  constexpr int RP = 16 * 16 * NT16 * 4 <= AITEMS * 16 ? 16
+                     : 8 * 16 * NT16 * 4 <= AITEMS * 16 ? 8 : 4;
+  static_assert(RP * 16 * NT16 * 4 <= AITEMS * 16, "k_gemm_dma: epilogue staging");
+  wide_epilogue<MBW, TN, E2M1, RP, WN>(a, acc, (float *)sA0, m0, bn, w, n16, kq);
+}
+
 // Sum of the K-split partials of k_gemm_lds in slice order (deterministic), then the row and
 // column exponents and the bias: C[m][n] = 2^(rowexp[m] + ce[n]) * sum_z part[z][m][n] + bias[n]
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ part, int nz,
@@ -1250,6 +1535,23 @@ void launch_lds(const GemmArgs &a, int cfg, dim3 grid, hipStream_t st) {
     case LDS_256x128: launch_lds1<KIND, NP, 128, 2, 4, 2, 4, 2>(a, grid, st); break;
     default: launch_lds1<KIND, NP, 64, 2, 2, 2, 4, 2>(a, grid, st); break;
   }
+}
+
+template <int KIND, int NP, int TN, int MB, int WN>
+void launch_dma1(const GemmArgs &a, dim3 grid, hipStream_t st) {
+  // 4 waves (one per SIMD): every A fragment of a chunk read up front, scheduled interleave;
+  // 8 waves (two per SIMD): A fragments read per step (register budget of two waves)
+  k_gemm_dma<KIND, NP, TN, MB, WN == 4, WN><<<grid, 64 * WN, 0, st>>>(a);
+}
+// shapes of k_gemm_dma: 128 rows x 192 columns (4 waves) or x 384 columns (8 waves); two A
+// pieces (f32 rows) use 64-row tiles, the largest whose four A buffers fit the LDS
+template <int KIND, int NP>
+void launch_dma(const GemmArgs &a, int wn, dim3 grid, hipStream_t st) {
+  constexpr int MB = NP == 1 ? 8 : 4;
+  if (wn == 8)
+    launch_dma1<KIND, NP, 3, MB, 8>(a, grid, st);
+  else
+    launch_dma1<KIND, NP, 3, MB, 4>(a, grid, st);
 }
 
 template <int KIND, bool SPLIT, bool SCF16, bool STEPM, bool PS, int MB>
@@ -1409,6 +1711,34 @@ static LdsPlan lds_plan(const sglq_dev *d, int64_t M) {
   return p;
 }
 
+// k_gemm_dma plan of a dense call.  Taken where it measured faster than k_gemm_lds: K of at
+// most 4096 and enough tiles to give most CUs one workgroup without a split over K (no
+// partial sums).  8 waves (384 columns) when that alone gives 200 tiles, else 4 waves (192
+// columns).  Measured (graph replay, GPTQ int4 g128 [11008, 4096], bf16 rows, incl. the A
+// prep): M = 512 95.5 -> 86.5 us, 1024 175 -> 139 us, 2048 289 -> 274 us.  At K = 11008 and
+// where a split over K is needed it measured slower, so those stay on k_gemm_lds.
+// SGLQ_GEMM_DMA=0 keeps every call on k_gemm_lds (A/B measurement).
+struct WidePlan {
+  int use, mb, wn;  // wn waves along N
+};
+static WidePlan wide_plan(const sglq_dev *d, int64_t M, int np) {
+  WidePlan p = {0, np == 1 ? 8 : 4, 4};
+  static int env = -1;
+  if (env < 0) {
+    const char *e = getenv("SGLQ_GEMM_DMA");
+    env = e ? atoi(e) : 1;
+  }
+  if (!env || !lds_direct(d) || M <= 64 || d->K > 4096) return p;
+  const int64_t bmr = 16 * p.mb, nbm = (M + bmr - 1) / bmr;
+  if (nbm * ((d->N + 383) / 384) >= 200) {
+    p.use = 1;
+    p.wn = 8;
+  } else if (nbm * ((d->N + 191) / 192) >= 200) {
+    p.use = 1;
+  }
+  return p;
+}
+
 int64_t sglq_gemm_rows(const sglq_dev *d, int split) {
   (void)d;
   (void)split;
@@ -1468,6 +1798,33 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
   if (grp && grp->swiglu && (!lds_direct(d) || grp->swiglu % 16 != 0)) {
     sglq_log_error("grouped GEMM: the fused SwiGLU needs the LDS kernel and mi %% 16 == 0");
     return -1;
+  }
+  if (!grp) {
+    const WidePlan wp = wide_plan(d, M, split ? 2 : 1);
+    if (wp.use) {
+      const int64_t bmr = 16 * wp.mb, cols = 48 * wp.wn;
+      a.nbm = (int)((M + bmr - 1) / bmr);
+      a.nbn = (int)((d->N + cols - 1) / cols);
+      a.part = nullptr;
+      a.xmap = 0;
+      const dim3 grid2((unsigned)(8 * ((a.nbm * a.nbn + 7) / 8)));
+      switch (d->kind) {
+        case SGLQ_KIND_U4:
+          if (split) launch_dma<SGLQ_KIND_U4, 2>(a, wp.wn, grid2, st);
+          else launch_dma<SGLQ_KIND_U4, 1>(a, wp.wn, grid2, st);
+          break;
+        case SGLQ_KIND_U8:
+          if (split) launch_dma<SGLQ_KIND_U8, 2>(a, wp.wn, grid2, st);
+          else launch_dma<SGLQ_KIND_U8, 1>(a, wp.wn, grid2, st);
+          break;
+        default:
+          if (split) launch_dma<SGLQ_KIND_E2M1, 2>(a, wp.wn, grid2, st);
+          else launch_dma<SGLQ_KIND_E2M1, 1>(a, wp.wn, grid2, st);
+          break;
+      }
+      SGLQ_HIP(hipGetLastError());
+      return 0;
+    }
   }
   // direct formats with f16-exact scales: the LDS-dequant kernel
   if (lds_direct(d)) {
@@ -1557,12 +1914,15 @@ static void gemm_ws_layout(const sglq_dev *d, int dt, int64_t M, int64_t *Mpad_o
   const int split = dt == SGLQ_DT_F32;
   // rows of A operands: whole row tiles of the LDS kernel's tiling (it reads no further), else
   // whole 128- and 256-row blocks
-  const int64_t rt = lds_direct(d) ? lds_rows(lds_plan(d, M).cfg) : 256;
+  const WidePlan wp = wide_plan(d, M, split ? 2 : 1);
+  const int64_t rt = wp.use ? std::max<int64_t>(16 * wp.mb, lds_rows(lds_plan(d, M).cfg))
+                    : lds_direct(d) ? lds_rows(lds_plan(d, M).cfg) : 256;
   const int64_t Mpad = (M + rt - 1) / rt * rt;
   *Mpad_out = Mpad;
   *aop_bytes = sglq_aop_bytes(d, Mpad, split);
   *o_part = (*aop_bytes + (size_t)Mpad * sizeof(int) + 255) / 256 * 256;
-  *part_bytes = lds_direct(d) ? (size_t)lds_plan(d, M).nz * M * d->N * sizeof(float) : 0;
+  const int nz = wp.use ? 1 : lds_direct(d) ? lds_plan(d, M).nz : 0;
+  *part_bytes = (size_t)nz * M * d->N * sizeof(float);
 }
 
 size_t sglq_gemm_ws_bytes(const sglq_dev *d, int dt, int64_t M) {
