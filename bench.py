@@ -243,7 +243,8 @@ def ceilings(torch, warmup):
     def st():
         return C.c_void_p(torch.cuda.current_stream().cuda_stream)
     res = {}
-    for nbytes, tag in ((23425024, "stream_read_23.4MB"), (1 << 30, "stream_read_1GiB")):
+    for nbytes, tag in ((23425024, "stream_read_23.4MB"), (4377600, "stream_read_4.38MB"),
+                        (1 << 30, "stream_read_1GiB")):
         n16 = nbytes // 16
         copies = max(1, math.ceil(ROTATE_BYTES / nbytes))
         bufs = [torch.ones(n16 * 4, dtype=torch.int32, device="cuda") for _ in range(copies)]
