@@ -42,7 +42,7 @@ __device__ __forceinline__ constexpr int kofs4(int i) { return (i >> 1) + 4 * (i
 //   MODE 0  A[m]                           (dense)
 //   MODE 1  A[rowmap[m]], zero if < 0       (MoE: token of each expert-sorted row)
 //   MODE 2  a_k = silu(A[m][k]) * A[m][kcols + k], A f32 (MoE: SwiGLU of the gate/up product,
-//           silu(g) = g / (1 + expf(-g)) as reference src/deepseek.c:662-663)
+//           silu(g) = g / (1 + e^-g) as reference src/deepseek.c:662-663, sglq_silu)
 // k_rowexp: one wave per row finds its largest |a| and the exact power of two that puts it in
 // [2^13, 2^14).  k_prep_a: workgroups of 16 rows x 64 items write the scaled f16 operands with
 // consecutive threads on consecutive rows of one 16-B item (Aop keeps the rows of an item
@@ -59,7 +59,7 @@ template <int MODE>
 __device__ __forceinline__ float prep_value(const void *A, int dt, int64_t rb, int kcols, int k) {
   if constexpr (MODE == 2) {
     const float g = ((const float *)A)[rb + k];
-    return (g / (1.0f + expf(-g))) * ((const float *)A)[rb + kcols + k];
+    return sglq_silu(g) * ((const float *)A)[rb + kcols + k];
   } else {
     return act_at(A, dt, rb + k);
   }
@@ -647,8 +647,8 @@ __device__ __forceinline__ void lds_epilogue(const GemmArgs &a, const float4_t (
                                              int mr0, int mend, int bn, int wn,
                                              const uint8_t *colexp, int n16, int kq) {
   if (a.swiglu) {
-    // MoE gate/up: C[m][n] = silu(g) * u with g, u the gate and up outputs (g / (1 + expf(-g))
-    // as reference src/deepseek.c:662-663), and the row maxima of |C| for the next prep
+    // MoE gate/up: C[m][n] = silu(g) * u with g, u the gate and up outputs (sglq_silu,
+    // g / (1 + e^-g) as reference src/deepseek.c:662-663), and the row maxima of |C|
     const int tg = bn * (NT16 / 2) + wn * (TN / 2), mi = a.swiglu;
     float rmx[MB][4];
 #pragma unroll
@@ -669,7 +669,7 @@ __device__ __forceinline__ void lds_epilogue(const GemmArgs &a, const float4_t (
           if (m < mend) {
             const float g = ldexpf(acc[i][2 * pj][r], a.rowexp[m] + ceg);
             const float u = ldexpf(acc[i][2 * pj + 1][r], a.rowexp[m] + ceu);
-            const float v = (g / (1.0f + expf(-g))) * u;
+            const float v = sglq_silu(g) * u;
             a.C[(int64_t)m * a.ldc + n] = v;
             rmx[i][r] = fmaxf(rmx[i][r], fabsf(v));
           }

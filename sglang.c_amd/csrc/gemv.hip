@@ -55,6 +55,10 @@ struct GemvArgs {
   const float *cw;
   float *cout;
   int ck;
+  // one token: slot j is segment {ids[j], row j, 1 row} if 0 <= ids[j] < nexp (segs, nseg,
+  // rowmap and cpos unused; the token row is A row 0)
+  const int32_t *ids;
+  int nid, nexp;
 };
 
 
@@ -69,7 +73,7 @@ __device__ __forceinline__ float act1(const void *A, int dt, int64_t i) {
 // K % 8 != 0, SwiGLU rows).
 __device__ __forceinline__ float swiglu_at(const GemvArgs &a, int64_t rb, int k) {
   const float g = ((const float *)a.A)[rb + k];  // silu as reference src/deepseek.c:662-663
-  return (g / (1.0f + expf(-g))) * ((const float *)a.A)[rb + a.kcols + k];
+  return sglq_silu(g) * ((const float *)a.A)[rb + a.kcols + k];
 }
 
 __device__ __forceinline__ void load8(const GemvArgs &a, int64_t row, int kp, float v[8]) {
@@ -558,16 +562,27 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
   int M = a.M, row0 = 0;
   const u32x4_t *codes = a.codes;
   const void *meta = a.meta;
+  int ns = 0;
   if constexpr (GRP != 0) {
-    const int ns = *a.nseg;
+    int4 sg;
+    bool live;
+    if (a.ids) {  // one token: slot blockIdx.y, its expert straight from the routing
+      for (int j = 0; j < a.nid; j++) ns += a.ids[j] >= 0 && a.ids[j] < a.nexp;
+      const int y = (int)blockIdx.y, e = y < a.nid ? a.ids[y] : -1;
+      live = e >= 0 && e < a.nexp;
+      sg = make_int4(e, y, 1, 0);
+    } else {
+      ns = *a.nseg;
+      live = (int)blockIdx.y < ns;
+      if (live) sg = a.segs[blockIdx.y];
+    }
     if (GRP == 2 && a.cout && ns == 0) {
       // no routed slot: the combined row is zero
       const int n = (cg * a.tpg) * 16 + lane;
       if (blockIdx.y == 0 && w == 0 && lane < 16 && n < a.N) a.cout[n] = 0.f;
       return;
     }
-    if ((int)blockIdx.y >= ns) return;
-    const int4 sg = a.segs[blockIdx.y];
+    if (!live) return;
     row0 = sg.y;
     M = sg.z;
     codes = a.codes_e[sg.x];
@@ -592,7 +607,8 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
     if (64 * q < nit) {  // wave-uniform
       // element offset in 32 bits (the host keeps the activation block under 2^31 elements)
       const int r = row0 + min(m, M - 1);
-      const uint32_t src = GRP == 1 && a.amode == 1 ? (uint32_t)a.rowmap[r] : (uint32_t)r;
+      const uint32_t src =
+          GRP == 1 && a.amode == 1 ? (a.ids ? 0u : (uint32_t)a.rowmap[r]) : (uint32_t)r;
       const uint32_t off = src * (uint32_t)a.lda + (ok[q] ? kp : 0);
       const u32x4_t *p = (const u32x4_t *)((const char *)a.A + off * (FOLD ? 4 : 2));
 #pragma unroll
@@ -614,7 +630,7 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
       float x;
       if constexpr (SWI) {
         const float g = __uint_as_float(raw[q][o >> 2][o & 3]);  // reference deepseek.c:662-663
-        x = (g / (1.0f + expf(-g))) * __uint_as_float(raw[q][RW + (o >> 2)][o & 3]);
+        x = sglq_silu(g) * __uint_as_float(raw[q][RW + (o >> 2)][o & 3]);
       } else if constexpr (FOLD)
         x = __uint_as_float(raw[q][o >> 2][o & 3]);
       else if (a.adt == SGLQ_DT_BF16)
@@ -726,7 +742,7 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
       int last = 0;
       if (lane == 0)
         last = __hip_atomic_fetch_add(&a.cnt[t], 1, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT) == *a.nseg - 1;
+                                      __HIP_MEMORY_SCOPE_AGENT) == ns - 1;
       last = __shfl(last, 0);
       if (!last) return;
       if (lane < 16 && n < a.N) {
@@ -739,7 +755,11 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
           float wj[8], vj[8];
 #pragma unroll
           for (int u = 0; u < 8; u++) {
-            rj[u] = j0 + u < a.ck ? a.cpos[j0 + u] : -1;
+            const int j = j0 + u;
+            if (a.ids)  // one token: slot j's row is row j
+              rj[u] = j < a.ck && a.ids[j] >= 0 && a.ids[j] < a.nexp ? j : -1;
+            else
+              rj[u] = j < a.ck ? a.cpos[j] : -1;
             wj[u] = j0 + u < a.ck ? a.cw[j0 + u] : 0.f;
           }
 #pragma unroll
@@ -1132,13 +1152,41 @@ int sglq_gemv_grouped_fits(const sglq_dev *d, int64_t max_rows, int split) {
   return max_rows <= 16 && plan_gemv(d, max_rows, split, true).S == 1;
 }
 
+// the grouped launch takes the wave-staged kernel: segments of at most 4 rows with K in one
+// workgroup's 8 slices, aligned identity-order rows (SwiGLU rows: f32 gate and up halves, both
+// 16-byte aligned)
+static bool grouped_aligned(const sglq_dev *d, bool split, const void *A, int64_t a_rows,
+                            int64_t lda) {
+  const int64_t esz = split ? 4 : 2;
+  return d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 && (lda * esz) % 16 == 0 &&
+         a_rows * lda < (1ll << 31);
+}
+static bool grouped_wave_ok(const sglq_dev *d, int64_t max_rows, bool split, int amode,
+                            const void *A, int64_t a_rows, int64_t lda, int kcols) {
+  return max_rows <= 4 && grouped_aligned(d, split, A, a_rows, lda) && d->nchunk <= 32 &&
+         (amode != 2 || (split && kcols % 4 == 0 && a_rows * lda + kcols < (1ll << 31)));
+}
+// ... and the one-token down launch also does the combine (arrival counters per tile, one K
+// range per workgroup)
+static bool grouped_combine_ok(const sglq_dev *d, int64_t max_rows, bool split, int amode) {
+  return max_rows == 1 && amode == 2 && d->gv_cnt && plan_gemv(d, 1, split, true, true).S == 1;
+}
+
+int sglq_moe_direct_ok(const sglq_dev *g0, const sglq_dev *d0, const void *h, int h_dtype,
+                       int64_t E, const void *gu, int64_t k, int64_t mi) {
+  const bool split1 = h_dtype == SGLQ_DT_F32;
+  return sglq_gemv_grouped_fits(g0, 1, split1) && sglq_gemv_grouped_fits(d0, 1, 1) &&
+         grouped_wave_ok(g0, 1, split1, 1, h, 1, E, 0) &&
+         grouped_wave_ok(d0, 1, true, 2, gu, k, 2 * mi, (int)mi) &&
+         grouped_combine_ok(d0, 1, true, 2);
+}
+
 int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows,
                       int64_t max_segs, const void *A, int dt, int64_t a_rows, int64_t lda,
                       int amode, const int32_t *rowmap, int kcols, float *C, int64_t ldc,
                       hipStream_t st, const sglq_combine *cmb) {
   const bool split = dt == SGLQ_DT_F32;
   const Plan pl = plan_gemv(d, max_rows, split, true);
-  const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
   if (pl.S != 1 || max_rows > 16) {
     sglq_log_error("qlinear: grouped GEMV needs one K range per workgroup (rows %lld)",
                    (long long)max_rows);
@@ -1152,30 +1200,38 @@ int sglq_gemv_grouped(const sglq_dev *d, const sglq_group *grp, int64_t max_rows
   a.rowmap = rowmap;
   a.amode = amode;
   a.kcols = kcols;
-  const bool aligned = d->kident && d->K % 8 == 0 && (uintptr_t)A % 16 == 0 &&
-                       (lda * esz) % 16 == 0 && a_rows * lda < (1ll << 31);
-  // segments of at most 4 rows (decode of 1-4 tokens): the wave-staged kernel, SwiGLU rows
-  // included (f32 gate and up halves, both 16-byte aligned), while K fits one workgroup's 8
-  // slices.  DeepSeek MoE decode (64 experts, top-6): T = 1 23.2 -> 21.7 us, T = 4 51.4 -> 43.5
-  if (max_rows <= 4 && aligned && d->nchunk <= 32 &&
-      (amode != 2 || (split && kcols % 4 == 0 && a_rows * lda + kcols < (1ll << 31)))) {
+  // segments of at most 4 rows (decode of 1-4 tokens): the wave-staged kernel.  DeepSeek MoE
+  // decode (64 experts, top-6): T = 1 23.2 -> 21.7 us, T = 4 51.4 -> 43.5
+  if (grouped_wave_ok(d, max_rows, split, amode, A, a_rows, lda, kcols)) {
     const Plan pw = plan_gemv(d, 1, split, true, true);  // 4-chunk slices
     GemvArgs aw = a;
     aw.S = pw.S;
     aw.ncg = pw.ncg;
     aw.ks = pw.ks;
     aw.tpg = pw.tpg;
-    // the combine needs an arrival counter per tile (allocated with the split-K state)
-    if (cmb && max_rows == 1 && amode == 2 && d->gv_cnt && pw.S == 1) {
+    if (grp->ids) {
+      aw.ids = grp->ids;
+      aw.nid = grp->nid;
+      aw.nexp = grp->nexp;
+    }
+    if (cmb && grouped_combine_ok(d, max_rows, split, amode)) {
       aw.cpos = cmb->pos;
       aw.cw = cmb->wts;
       aw.cout = cmb->out;
       aw.ck = cmb->k;
       *cmb->done = 1;
+    } else if (grp->ids && amode == 2) {
+      sglq_log_error("qmoe: one-token segments without the fused combine");
+      return -1;
     }
     return launch_gemv_wave(d, aw, pw, split, (unsigned)max_segs, st);
   }
-  return launch_gemv(d, a, pl, split, amode != 2 && aligned, (unsigned)max_segs, st);
+  if (grp->ids) {
+    sglq_log_error("qmoe: one-token segments need the wave-staged grouped GEMV");
+    return -1;
+  }
+  return launch_gemv(d, a, pl, split, amode != 2 && grouped_aligned(d, split, A, a_rows, lda),
+                     (unsigned)max_segs, st);
 }
 
 // C = A W^T (+ bias): decode GEMV up to 16 rows (and 17-32 rows as two GEMVs), prefill GEMM

@@ -218,12 +218,23 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
         T <= 4 && sglq_gemv_grouped_fits(g0, T, split1) && sglq_gemv_grouped_fits(d0, T, 1);
     const bool fuse = !decode && sglq_gemm_lds_direct(g0) && mi % 16 == 0;
     int *rowmax = fuse ? (int *)(ws + o_rmax) : nullptr;
-    k_moe_route<<<1, 1024, 0, st>>>(topk_ids, (int)P, k, n_exp, SGLQ_MOE_BM, rowmap, pos, segs,
-                                    nseg, rowmax);
-    SGLQ_HIP(hipGetLastError());
+    // one token whose grouped GEMVs can read its routing directly (slot j = segment j): no
+    // routing kernel (DeepSeek MoE decode, T = 1: one launch of ~2-4 us fewer)
+    const bool direct = decode && T == 1 &&
+                        sglq_moe_direct_ok(g0, d0, h, h_dtype, E, gu, k, mi);
+    if (!direct) {
+      k_moe_route<<<1, 1024, 0, st>>>(topk_ids, (int)P, k, n_exp, SGLQ_MOE_BM, rowmap, pos,
+                                      segs, nseg, rowmax);
+      SGLQ_HIP(hipGetLastError());
+    }
     sglq_group g1 = {dp, dp + n_exp, (const uint8_t *const *)(dp + 2 * n_exp), segs, nseg};
     sglq_group g2 = {dp + 3 * n_exp, dp + 4 * n_exp, (const uint8_t *const *)(dp + 5 * n_exp),
                      segs, nseg};
+    if (direct) {
+      g1.ids = g2.ids = topk_ids;
+      g1.nid = g2.nid = (int)k;
+      g1.nexp = g2.nexp = n_exp;
+    }
     // decode-sized batches (every expert has at most T <= 4 rows): grouped GEMVs that read the
     // token rows and the SwiGLU rows directly; otherwise operand prep + grouped GEMMs
     int combined = 0;

@@ -192,7 +192,7 @@ __global__ __launch_bounds__(64) void k_moe_gate(const float *__restrict__ logit
   }
 }
 
-// act[t][c] = silu(g) * u with silu(g) = g / (1 + expf(-g)) rounded first, as the reference's
+// act[t][c] = silu(g) * u with silu(g) = g / (1 + e^-g) (sglq_silu) rounded first, as the reference's
 // sgl_silu_inplace followed by the product (reference src/ops.c:288-293, src/llama.c:1172-1173)
 __global__ void k_swiglu(const float *__restrict__ g, int64_t ldg, const float *__restrict__ u,
                          int64_t ldu, int64_t T, int64_t I, float *__restrict__ act) {
@@ -200,7 +200,7 @@ __global__ void k_swiglu(const float *__restrict__ g, int64_t ldg, const float *
   if (i >= T * I) return;
   const int64_t t = i / I, c = i - t * I;
   const float x = g[t * ldg + c];
-  const float s = x / (1.0f + expf(-x));
+  const float s = sglq_silu(x);
   act[i] = s * u[t * ldu + c];
 }
 

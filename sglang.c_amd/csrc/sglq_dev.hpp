@@ -135,6 +135,10 @@ struct sglq_group {               // per-expert weights (device arrays) + device
   const int *nseg;                // blocks in use (device scalar)
   int swiglu;                     // gate/up weights [2 mi, K]: mi > 0 = C gets silu(g) * u
   int *rowmax;                    // with swiglu: per-row max |C| bits (atomic max, preset 0)
+  // one token (decode GEMVs only): segments straight from its routing, slot j = segment
+  // {ids[j], row j, 1 row} when 0 <= ids[j] < nexp (segs, nseg and the row map are not used)
+  const int32_t *ids;
+  int nid, nexp;
 };
 // A operands of Mpad rows into aop (sglq_aop_bytes) + row exponents; mode 0 dense rows,
 // 1 rows gathered through rowmap (-1 = zero row), 2 silu(A[m][k]) * A[m][kcols + k] (f32 A).
@@ -155,6 +159,11 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop, con
 // rowmap[r], 2 silu(A[r][k]) * A[r][kcols + k] with f32 A; A has a_rows rows).  Only when every workgroup can take
 // all of K (sglq_gemv_grouped_fits).
 int sglq_gemv_grouped_fits(const sglq_dev *d, int64_t max_rows, int split);
+// The one-token MoE decode can take its segments straight from the routing (no routing
+// kernel): both grouped launches take the wave-staged kernel and the down launch fuses the
+// combine.  h: token row (h_dtype, E elements); gu: the gate/up output [k][2 mi] (f32).
+int sglq_moe_direct_ok(const sglq_dev *gate_up, const sglq_dev *down, const void *h,
+                       int h_dtype, int64_t E, const void *gu, int64_t k, int64_t mi);
 // cmb (optional, one token): the down launch also forms out[n] = sum_j wts[j] * C[pos[j]][n]
 // in slot order when its kernel can (then *cmb->done is set to 1, else left alone).
 struct sglq_combine {
@@ -181,6 +190,14 @@ __host__ __device__ __forceinline__ int64_t sglq_mofs(int64_t u) { return (u >> 
 __host__ __device__ __forceinline__ int64_t sglq_ebyte(int64_t t, int n16, int64_t s,
                                                       int64_t nmeta) {
   return t * nmeta * 16 + (s >> 4) * 256 + n16 * 16 + (s & 15);
+}
+
+// silu(g) = g / (1 + e^-g) (reference src/deepseek.c:662-663) with the hardware exponential
+// and reciprocal (v_exp_f32 on -g log2(e), v_rcp_f32): about 1e-6 relative error against
+// the libm form, which costs ~20 VALU per element (exp range reduction and an IEEE divide).
+// The MoE blocks are compared with the reference within 1e-3; routing scores keep libm expf.
+__device__ __forceinline__ float sglq_silu(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.44269504088896341f));
 }
 
 __device__ __forceinline__ float sglq_e2m1_value(uint32_t c) {
