@@ -1,6 +1,7 @@
 // gemv_row.hip — one-row decode GEMV (M = 1) with a lean issue budget.
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include "gemv_ops.hpp"
 
@@ -33,6 +34,18 @@ struct RowArgs {
   const float *bias;
   float *C;
   int N, K, ntile, nchunk, nmeta, cpg, ksl, adt;
+  // grouped one-token MoE launches (GRP 1 gate/up, GRP 2 down): blockIdx.y = routing slot j,
+  // expert ids[j] (slots with ids[j] outside [0, nexp) are empty); C row j is written (ldc).
+  // GRP 2 reads silu(A[j][k]) * A[j][kcols + k] of the f32 gate/up rows (lda) and the last
+  // slot to finish a tile writes cout[n] = sum over slots of cw[j] * C[j][n], in slot order.
+  const u32x4_t *const *codes_e;
+  const void *const *meta_e;
+  const int32_t *ids;
+  const float *cw;
+  float *cout;
+  int *cnt;
+  int64_t lda, ldc;
+  int nid, nexp, kcols;
 };
 
 // 32 zero bytes: the activation item of a lane whose item lies past K (or past the wave's
@@ -41,8 +54,10 @@ __device__ const u32x4_t g_zero_item[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
 
 typedef __attribute__((address_space(1))) const u32x4_t GU4;
 
-template <int KIND, int CPW, int TPW, int DT, bool SCF16, bool MV, int NW>
+template <int KIND, int CPW, int TPW, int DT, bool SCF16, bool MV, int NW, int GRP = 0>
 __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
+  static_assert(GRP != 2 || DT == SGLQ_DT_F32, "SwiGLU rows are f32");
+  static_assert(GRP == 0 || (TPW == 1 && KIND != SGLQ_KIND_E2M1), "grouped: one tile per wave");
   constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
   constexpr int NP = DT == SGLQ_DT_BF16 ? 1 : 2;     // f16 operand rows: hi (+ lo)
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;  // MFMA steps per chunk
@@ -65,13 +80,39 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
   const int nch = t0 < a.ntile && c0 < a.nchunk ? min(CPW, a.nchunk - c0) : 0;
   const int cb = nch > 0 ? c0 : 0;
   const int n16 = lane & 15, kq = lane >> 4;
+  // grouped: this workgroup's routing slot and its expert's weights
+  const u32x4_t *codes = a.codes;
+  const void *meta = a.meta;
+  const char *arow = (const char *)a.A;
+  float *crow = a.C;
+  int ns = 0;
+  if constexpr (GRP != 0) {
+    for (int j = 0; j < a.nid; j++) ns += a.ids[j] >= 0 && a.ids[j] < a.nexp;
+    const int y = (int)blockIdx.y, e = y < a.nid ? a.ids[y] : -1;
+    if (GRP == 2 && ns == 0) {  // no routed slot: the combined row is zero
+      if (y == 0 && sl == 0 && kq == 0) {
+#pragma unroll
+        for (int u = 0; u < TPW; u++) {
+          const int n = (t0 + u) * 16 + n16;
+          if (t0 + u < a.ntile && n < a.N) a.cout[n] = 0.f;
+        }
+      }
+      return;
+    }
+    if (e < 0 || e >= a.nexp) return;  // workgroup-uniform
+    codes = a.codes_e[e];
+    meta = a.meta_e[e];
+    if (GRP == 2) arow += (int64_t)y * a.lda * 4;
+    crow += (int64_t)y * a.ldc;
+  }
   int tl[TPW];  // tiles, clamped to the last (valid memory; results past it are not stored)
 #pragma unroll
   for (int u = 0; u < TPW; u++) tl[u] = min(t0 + u, a.ntile - 1);
 
   // ---- loads: activations, meta, codes (all issued before any is used)
   constexpr int RW = DT == SGLQ_DT_F32 ? 2 : 1;  // 128-bit words per 8-element item
-  u32x4_t raw[NQ][RW];
+  constexpr int RU = GRP == 2 ? RW : 0;          // and as many of the up half (SwiGLU rows)
+  u32x4_t raw[NQ][RW + RU];
 #pragma unroll
   for (int q = 0; q < NQ; q++) {
     const int it = 64 * q + lane;
@@ -79,10 +120,15 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
     const bool ok = nch > 0 && it < IPW && k < a.K;
     // global address space on both sides of the select keeps these global (not flat) loads,
     // which the staging can wait for without waiting for the weights behind them
-    const GU4 *p = ok ? (const GU4 *)((const char *)a.A + (int64_t)k * (RW * 2))
-                      : (const GU4 *)g_zero_item;
+    const GU4 *p = ok ? (const GU4 *)(arow + (int64_t)k * (RW * 2)) : (const GU4 *)g_zero_item;
 #pragma unroll
     for (int i = 0; i < RW; i++) raw[q][i] = p[i];
+    if constexpr (GRP == 2) {
+      const GU4 *pu = ok ? (const GU4 *)(arow + ((int64_t)a.kcols + k) * 4)
+                         : (const GU4 *)g_zero_item;
+#pragma unroll
+      for (int i = 0; i < RW; i++) raw[q][RW + i] = pu[i];
+    }
   }
   MT mv[TPW][CPW];  // meta entry (e8m0 bytes of four steps) of every chunk
   uint32_t cexp[TPW];
@@ -94,7 +140,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
       // (32 for 8-byte entries) of the quads cb/4 .. , clamped to the row
       constexpr int ESZ = sizeof(MT);
       const int64_t nm = E2M1 ? a.nmeta / 4 : a.nmeta;  // entries per column
-      const MT *mp = (const MT *)a.meta + sglq_mrow(tl[u], n16, nm);
+      const MT *mp = (const MT *)meta + sglq_mrow(tl[u], n16, nm);
       const int q0 = cb >> 2, qlast = (int)(nm >> 2) - 1;
 #pragma unroll
       for (int v = 0; v < CPW / 4; v++) {
@@ -115,7 +161,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
       // groups of cpg chunks (or slices not aligned to quads): the entry of chunk cb + i is
       // group (cb + i) / cpg, found with scalar arithmetic
       const int cpg = E2M1 ? 1 : a.cpg;
-      const MT *mp = (const MT *)a.meta + sglq_mrow(tl[u], n16, E2M1 ? a.nmeta / 4 : a.nmeta);
+      const MT *mp = (const MT *)meta + sglq_mrow(tl[u], n16, E2M1 ? a.nmeta / 4 : a.nmeta);
       int g = cb / cpg, r = cb - g * cpg;
 #pragma unroll
       for (int i = 0; i < CPW; i++) {
@@ -133,7 +179,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
     const int last = nch > 0 ? nch - 1 : 0;
 #pragma unroll
     for (int u = 0; u < TPW; u++) {
-      const u32x4_t *cp = a.codes + ((int64_t)tl[u] * a.nchunk + cb) * 64 + lane;
+      const u32x4_t *cp = codes + ((int64_t)tl[u] * a.nchunk + cb) * 64 + lane;
 #pragma unroll
       for (int i = 0; i < CPW; i++) wv[u][i] = __builtin_nontemporal_load(cp + min(i, last) * 64);
     }
@@ -144,7 +190,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
   auto decode = [&](int q, float (&v)[8]) {
 #pragma unroll
     for (int o = 0; o < 8; o++) {
-      if constexpr (DT == SGLQ_DT_F32)
+      if constexpr (GRP == 2)  // silu(gate) * up (reference src/deepseek.c:662-663)
+        v[o] = sglq_silu(__uint_as_float(raw[q][o >> 2][o & 3])) *
+               __uint_as_float(raw[q][RW + (o >> 2)][o & 3]);
+      else if constexpr (DT == SGLQ_DT_F32)
         v[o] = __uint_as_float(raw[q][o >> 2][o & 3]);
       else if constexpr (DT == SGLQ_DT_F16)
         v[o] = f16_bits((raw[q][0][o >> 1] >> (16 * (o & 1))) & 0xFFFFu);
@@ -268,27 +317,68 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
   }
 
   // ---- K slices of a tile group added in slice order, then bias and store (lanes 0-15)
-  if (ks == 1) {
+  if (ks > 1) {
+    if (kq == 0) {
 #pragma unroll
-    for (int u = 0; u < TPW; u++) {
-      const int n = (t0 + u) * 16 + n16;
-      if (kq == 0 && t0 + u < a.ntile && n < a.N) a.C[n] = f[u] + (a.bias ? a.bias[n] : 0.f);
+      for (int u = 0; u < TPW; u++) s_sum[w][u][n16] = f[u];
     }
-    return;
-  }
-  if (kq == 0) {
+    __syncthreads();
+    if (sl != 0) return;
+    if (kq == 0) {
 #pragma unroll
-    for (int u = 0; u < TPW; u++) s_sum[w][u][n16] = f[u];
+      for (int u = 0; u < TPW; u++) {
+        float sum = s_sum[w][u][n16];
+        for (int q = 1; q < ks; q++) sum += s_sum[w + q][u][n16];
+        f[u] = sum;
+      }
+    }
   }
-  __syncthreads();
-  if (sl != 0 || kq != 0) return;
 #pragma unroll
   for (int u = 0; u < TPW; u++) {
     const int n = (t0 + u) * 16 + n16;
-    if (t0 + u >= a.ntile || n >= a.N) continue;
-    float sum = s_sum[w][u][n16];
-    for (int q = 1; q < ks; q++) sum += s_sum[w + q][u][n16];
-    a.C[n] = sum + (a.bias ? a.bias[n] : 0.f);
+    if (kq != 0 || t0 + u >= a.ntile || n >= a.N) continue;
+    if constexpr (GRP == 2)  // read back by another workgroup's combine: written through
+      __hip_atomic_store(&crow[n], f[u], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+      crow[n] = f[u] + (GRP == 0 && a.bias ? a.bias[n] : 0.f);
+  }
+  if constexpr (GRP == 2) {
+    // fused combine: the stores above are acknowledged before the arrival, and the last slot
+    // of the tile adds the rows ((0 + w0 o0) + w1 o1) + ... in slot order, as k_moe_combine
+    // (reference src/deepseek.c:675-676)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const int t = t0;
+    if (t >= a.ntile) return;
+    int last = 0;
+    if (lane == 0)
+      last = __hip_atomic_fetch_add(&a.cnt[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             ns - 1;
+    last = __shfl(last, 0);
+    if (!last) return;
+    const int n = t * 16 + n16;
+    if (lane < 16 && n < a.N) {
+      float sum = 0.f;
+      for (int j0 = 0; j0 < a.nid; j0 += 8) {
+        float wj[8], vj[8];
+        bool lj[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          const int j = j0 + u;
+          lj[u] = j < a.nid && a.ids[j] >= 0 && a.ids[j] < a.nexp;
+          wj[u] = lj[u] ? a.cw[j] : 0.f;
+          vj[u] = lj[u] ? __hip_atomic_load(&a.C[(int64_t)j * a.ldc + n], __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT)
+                        : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+          if (lj[u]) sum = __fadd_rn(sum, __fmul_rn(wj[u], vj[u]));
+      }
+      a.cout[n] = sum;
+    }
+    if (lane == 0) __hip_atomic_store(&a.cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -343,7 +433,89 @@ bool launch_row(const RowArgs &a, int cpw, int tpw, int nw, int dt, bool scf16, 
   return false;
 }
 
+// grouped one-token launch: f16 scales, one group per chunk (quad meta loads from 4 chunks),
+// 8 waves, cpw chunks per wave
+template <int KIND, int GRP, int DT>
+bool launch_row_grp2(const RowArgs &a, int cpw, dim3 grid, size_t lds, hipStream_t st) {
+  switch (cpw) {
+    case 1: k_gemv_row<KIND, 1, 1, DT, true, false, 8, GRP><<<grid, 512, lds, st>>>(a); return true;
+    case 2: k_gemv_row<KIND, 2, 1, DT, true, false, 8, GRP><<<grid, 512, lds, st>>>(a); return true;
+    case 4: k_gemv_row<KIND, 4, 1, DT, true, true, 8, GRP><<<grid, 512, lds, st>>>(a); return true;
+    case 8: k_gemv_row<KIND, 8, 1, DT, true, true, 8, GRP><<<grid, 512, lds, st>>>(a); return true;
+    default: return false;
+  }
+}
+template <int KIND>
+bool launch_row_grp(const RowArgs &a, int grp, int dt, int cpw, dim3 grid, size_t lds,
+                    hipStream_t st) {
+  if (grp == 2) return launch_row_grp2<KIND, 2, SGLQ_DT_F32>(a, cpw, grid, lds, st);
+  if (dt == SGLQ_DT_F32) return launch_row_grp2<KIND, 1, SGLQ_DT_F32>(a, cpw, grid, lds, st);
+  if (dt == SGLQ_DT_F16) return launch_row_grp2<KIND, 1, SGLQ_DT_F16>(a, cpw, grid, lds, st);
+  return launch_row_grp2<KIND, 1, SGLQ_DT_BF16>(a, cpw, grid, lds, st);
+}
+
 }  // namespace
+
+// Grouped one-token MoE launch on k_gemv_row (see RowArgs): 1 = launched, 0 = not applicable
+// (the caller takes the grouped k_gemv_wave), -1 = launch error.  grp 1: C row j = token row A
+// times expert ids[j]'s weights; grp 2: C row j = silu(A[j][:K]) * A[j][kcols:] times expert
+// ids[j]'s weights (f32 A, lda), and cout = the slot-order weighted sum of the rows.
+int sglq_gemv_row_grouped(const sglq_dev *d, const void *const *codes_e,
+                          const void *const *meta_e, const int32_t *ids, int k, int nexp,
+                          int grp, const void *A, int dt, int64_t lda, int kcols, float *C,
+                          int64_t ldc, const float *cw, float *cout, hipStream_t st) {
+  if (d->kind == SGLQ_KIND_E2M1 || !d->kident || d->K % 8 != 0 || !d->scf16 ||
+      d->meta_mode != SGLQ_META_GROUP || d->cpg != 1 || d->nchunk > 32)
+    return 0;
+  if ((uintptr_t)A % 16 != 0 || (grp == 2 && (dt != SGLQ_DT_F32 || lda % 4 != 0 ||
+                                              kcols % 4 != 0 || !d->gv_cnt || !cout)))
+    return 0;
+  if (const char *e = getenv("SGLQ_GEMV_ROW"))
+    if (atoi(e) == 0) return 0;
+  const int64_t nc = d->nchunk;
+  int cpw = 0;
+  for (int c : {1, 2, 4, 8})
+    if (!cpw && 8 * c >= nc) cpw = c;
+  if (!cpw) return 0;
+  int ksl = 0;
+  while ((1 << ksl) * cpw < nc && (2 << ksl) <= 8) ksl++;
+  RowArgs a;
+  memset(&a, 0, sizeof(a));
+  a.A = A;
+  a.C = C;
+  a.N = (int)d->N;
+  a.K = (int)d->K;
+  a.ntile = (int)d->ntile;
+  a.nchunk = (int)nc;
+  a.nmeta = (int)d->nmeta;
+  a.cpg = 1;
+  a.ksl = ksl;
+  a.adt = dt;
+  a.codes_e = (const u32x4_t *const *)codes_e;
+  a.meta_e = meta_e;
+  a.ids = ids;
+  a.nid = k;
+  a.nexp = nexp;
+  a.lda = lda;
+  a.ldc = ldc;
+  a.kcols = kcols;
+  a.cw = cw;
+  a.cout = cout;
+  a.cnt = d->gv_cnt;
+  const int tpg = 8 >> ksl;
+  const dim3 grid((unsigned)((d->ntile + tpg - 1) / tpg), (unsigned)k);
+  const int np = dt == SGLQ_DT_BF16 && grp == 1 ? 1 : 2;
+  const int spc = d->kind == SGLQ_KIND_U8 ? 2 : 4;
+  const size_t lds = (size_t)8 * np * (cpw * spc * 4 + 4) * 16;
+  const bool ok = d->kind == SGLQ_KIND_U8
+                      ? launch_row_grp<SGLQ_KIND_U8>(a, grp, dt, cpw, grid, lds, st)
+                      : launch_row_grp<SGLQ_KIND_U4>(a, grp, dt, cpw, grid, lds, st);
+  if (!ok) return 0;
+  SGLQ_HIP(hipGetLastError());
+  return 1;
+fail:
+  return -1;
+}
 
 // 1 = launched, 0 = this weight / row takes the general kernels, -1 = launch error
 int sglq_gemv_row(const sglq_dev *d, const void *A, int dt, const float *bias, float *C,

@@ -240,13 +240,27 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
     int combined = 0;
     if (decode) {
       const int64_t max_segs = P < n_exp ? P : n_exp;
-      if (sglq_gemv_grouped(g0, &g1, T, max_segs, h, h_dtype, T, E, 1, rowmap, 0, gu, 2 * mi,
-                            st) != 0)
+      // one token read straight from its routing: the one-row kernel where the weights allow
+      // (f16 group scales, one group per chunk), else the grouped wave-staged kernel
+      int r1 = 0, r2 = 0;
+      if (direct) {
+        r1 = sglq_gemv_row_grouped(g0, g1.codes, g1.meta, topk_ids, (int)k, n_exp, 1, h,
+                                   h_dtype, E, 0, gu, 2 * mi, nullptr, nullptr, st);
+        if (r1 < 0) return -1;
+      }
+      if (!r1 && sglq_gemv_grouped(g0, &g1, T, max_segs, h, h_dtype, T, E, 1, rowmap, 0, gu,
+                                   2 * mi, st) != 0)
         return -1;
+      if (direct) {
+        r2 = sglq_gemv_row_grouped(d0, g2.codes, g2.meta, topk_ids, (int)k, n_exp, 2, gu,
+                                   SGLQ_DT_F32, 2 * mi, (int)mi, o, E, topk_w, out, st);
+        if (r2 < 0) return -1;
+        combined = r2;
+      }
       // one token: the down launch also does the combine when it can
       const sglq_combine cb = {pos, topk_w, k, out, &combined};
-      if (sglq_gemv_grouped(d0, &g2, T, max_segs, gu, SGLQ_DT_F32, P, 2 * mi, 2, nullptr,
-                            (int)mi, o, E, st, T == 1 ? &cb : nullptr) != 0)
+      if (!r2 && sglq_gemv_grouped(d0, &g2, T, max_segs, gu, SGLQ_DT_F32, P, 2 * mi, 2, nullptr,
+                                   (int)mi, o, E, st, T == 1 ? &cb : nullptr) != 0)
         return -1;
     } else if (fuse) {
       // act[r] = silu(gate) * up of row r, [P, mi] f32, written by the gate/up GEMM together

@@ -104,10 +104,12 @@ def test_moe_prefill_deepseek_shape(orc):
 
 @pytest.mark.parametrize("fmt", ["gptq4", "mxfp4", "gptq8"])
 def test_moe_decode_one_token(orc, fmt):
-    """One token: one row per expert segment, so both grouped launches take the wave-staged
-    GEMV (token rows gathered for gate/up; SwiGLU rows formed while loading for down, and the
-    weighted combine done by the last segment of each tile), with and without unrouted slots,
-    and with none routed at all (zero output)."""
+    """One token: segments straight from the routing (no routing launch), one row per slot.
+    GPTQ4 (f16 scales, one group per chunk) takes the grouped one-row kernel, MXFP4 and GPTQ8
+    (two chunks per group) the grouped wave-staged kernel: token rows gathered for gate/up,
+    SwiGLU rows formed while loading for down, and the weighted combine done by the last slot
+    of each tile; with and without unrouted slots, and with none routed at all (zero
+    output)."""
     _check(orc, 8, 512, 256, 1, 3, seed=91, fmt=fmt)
     _check(orc, 6, 256, 384, 1, 4, seed=93, fmt=fmt, dtypes=("f32",), drop=True)
     _check(orc, 4, 256, 128, 1, 2, seed=95, fmt=fmt, dtypes=("bf16",), drop="all")
