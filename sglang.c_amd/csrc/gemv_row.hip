@@ -34,18 +34,20 @@ struct RowArgs {
   const float *bias;
   float *C;
   int N, K, ntile, nchunk, nmeta, cpg, ksl, adt;
-  // grouped one-token MoE launches (GRP 1 gate/up, GRP 2 down): blockIdx.y = routing slot j,
-  // expert ids[j] (slots with ids[j] outside [0, nexp) are empty); C row j is written (ldc).
-  // GRP 2 reads silu(A[j][k]) * A[j][kcols + k] of the f32 gate/up rows (lda) and the last
-  // slot to finish a tile writes cout[n] = sum over slots of cw[j] * C[j][n], in slot order.
+  // grouped MoE decode launches (GRP 1 gate/up, GRP 2 down) of nid / slots tokens read
+  // straight from the routing: blockIdx.y = pair j = (token j / slots, slot j % slots), expert
+  // ids[j] (pairs with ids[j] outside [0, nexp) are empty); C row j is written (ldc).  GRP 1
+  // reads token row j / slots of A (lda); GRP 2 reads silu(A[j][k]) * A[j][kcols + k] of the
+  // f32 gate/up rows (lda), and the last pair to finish a tile writes, for every token t,
+  // cout[t][n] (ldo) = sum over its slots s of cw[t slots + s] * C[t slots + s][n], in order.
   const u32x4_t *const *codes_e;
   const void *const *meta_e;
   const int32_t *ids;
   const float *cw;
   float *cout;
   int *cnt;
-  int64_t lda, ldc;
-  int nid, nexp, kcols;
+  int64_t lda, ldc, ldo;
+  int nid, nexp, kcols, slots;
 };
 
 // 32 zero bytes: the activation item of a lane whose item lies past K (or past the wave's
@@ -89,12 +91,13 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
   if constexpr (GRP != 0) {
     for (int j = 0; j < a.nid; j++) ns += a.ids[j] >= 0 && a.ids[j] < a.nexp;
     const int y = (int)blockIdx.y, e = y < a.nid ? a.ids[y] : -1;
-    if (GRP == 2 && ns == 0) {  // no routed slot: the combined row is zero
+    if (GRP == 2 && ns == 0) {  // no routed pair: the combined rows are zero
       if (y == 0 && sl == 0 && kq == 0) {
 #pragma unroll
         for (int u = 0; u < TPW; u++) {
           const int n = (t0 + u) * 16 + n16;
-          if (t0 + u < a.ntile && n < a.N) a.cout[n] = 0.f;
+          if (t0 + u < a.ntile && n < a.N)
+            for (int t = 0; t < a.nid / a.slots; t++) a.cout[t * a.ldo + n] = 0.f;
         }
       }
       return;
@@ -102,7 +105,10 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
     if (e < 0 || e >= a.nexp) return;  // workgroup-uniform
     codes = a.codes_e[e];
     meta = a.meta_e[e];
-    if (GRP == 2) arow += (int64_t)y * a.lda * 4;
+    if (GRP == 2)
+      arow += (int64_t)y * a.lda * 4;
+    else
+      arow += (int64_t)(y / a.slots) * a.lda * (DT == SGLQ_DT_F32 ? 4 : 2);
     crow += (int64_t)y * a.ldc;
   }
   int tl[TPW];  // tiles, clamped to the last (valid memory; results past it are not stored)
@@ -359,24 +365,27 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
     if (!last) return;
     const int n = t * 16 + n16;
     if (lane < 16 && n < a.N) {
-      float sum = 0.f;
-      for (int j0 = 0; j0 < a.nid; j0 += 8) {
-        float wj[8], vj[8];
-        bool lj[8];
+      for (int tok = 0; tok < a.nid / a.slots; tok++) {
+        const int jb = tok * a.slots;
+        float sum = 0.f;
+        for (int j0 = 0; j0 < a.slots; j0 += 8) {
+          float wj[8], vj[8];
+          bool lj[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-          const int j = j0 + u;
-          lj[u] = j < a.nid && a.ids[j] >= 0 && a.ids[j] < a.nexp;
-          wj[u] = lj[u] ? a.cw[j] : 0.f;
-          vj[u] = lj[u] ? __hip_atomic_load(&a.C[(int64_t)j * a.ldc + n], __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT)
-                        : 0.f;
+          for (int u = 0; u < 8; u++) {
+            const int j = jb + j0 + u;
+            lj[u] = j0 + u < a.slots && a.ids[j] >= 0 && a.ids[j] < a.nexp;
+            wj[u] = lj[u] ? a.cw[j] : 0.f;
+            vj[u] = lj[u] ? __hip_atomic_load(&a.C[(int64_t)j * a.ldc + n], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT)
+                          : 0.f;
+          }
+#pragma unroll
+          for (int u = 0; u < 8; u++)
+            if (lj[u]) sum = __fadd_rn(sum, __fmul_rn(wj[u], vj[u]));
         }
-#pragma unroll
-        for (int u = 0; u < 8; u++)
-          if (lj[u]) sum = __fadd_rn(sum, __fmul_rn(wj[u], vj[u]));
+        a.cout[tok * a.ldo + n] = sum;
       }
-      a.cout[n] = sum;
     }
     if (lane == 0) __hip_atomic_store(&a.cnt[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -456,22 +465,29 @@ bool launch_row_grp(const RowArgs &a, int grp, int dt, int cpw, dim3 grid, size_
 
 }  // namespace
 
-// Grouped one-token MoE launch on k_gemv_row (see RowArgs): 1 = launched, 0 = not applicable
-// (the caller takes the grouped k_gemv_wave), -1 = launch error.  grp 1: C row j = token row A
-// times expert ids[j]'s weights; grp 2: C row j = silu(A[j][:K]) * A[j][kcols:] times expert
-// ids[j]'s weights (f32 A, lda), and cout = the slot-order weighted sum of the rows.
-int sglq_gemv_row_grouped(const sglq_dev *d, const void *const *codes_e,
-                          const void *const *meta_e, const int32_t *ids, int k, int nexp,
-                          int grp, const void *A, int dt, int64_t lda, int kcols, float *C,
-                          int64_t ldc, const float *cw, float *cout, hipStream_t st) {
+// Grouped MoE decode launch on k_gemv_row (see RowArgs).  The weights and rows it takes:
+// f16 group scales, one group per chunk, K within 8 waves of at most 8 chunks, 16-byte
+// aligned rows (grp 2: f32 gate/up rows with 4-element aligned halves and arrival counters).
+int sglq_gemv_row_grouped_ok(const sglq_dev *d, int grp, const void *A, int dt, int64_t lda,
+                             int kcols) {
   if (d->kind == SGLQ_KIND_E2M1 || !d->kident || d->K % 8 != 0 || !d->scf16 ||
-      d->meta_mode != SGLQ_META_GROUP || d->cpg != 1 || d->nchunk > 32)
+      d->meta_mode != SGLQ_META_GROUP || d->cpg != 1 || d->nchunk > 64)
     return 0;
-  if ((uintptr_t)A % 16 != 0 || (grp == 2 && (dt != SGLQ_DT_F32 || lda % 4 != 0 ||
-                                              kcols % 4 != 0 || !d->gv_cnt || !cout)))
-    return 0;
+  const int64_t esz = dt == SGLQ_DT_F32 ? 4 : 2;
+  if ((uintptr_t)A % 16 != 0 || (lda * esz) % 16 != 0) return 0;
+  if (grp == 2 && (dt != SGLQ_DT_F32 || kcols % 4 != 0 || !d->gv_cnt)) return 0;
   if (const char *e = getenv("SGLQ_GEMV_ROW"))
     if (atoi(e) == 0) return 0;
+  return 1;
+}
+
+// 1 = launched, 0 = not applicable (sglq_gemv_row_grouped_ok), -1 = launch error.
+int sglq_gemv_row_grouped(const sglq_dev *d, const void *const *codes_e,
+                          const void *const *meta_e, const int32_t *ids, int npairs, int slots,
+                          int nexp, int grp, const void *A, int dt, int64_t lda, int kcols,
+                          float *C, int64_t ldc, const float *cw, float *cout, int64_t ldo,
+                          hipStream_t st) {
+  if (!sglq_gemv_row_grouped_ok(d, grp, A, dt, lda, kcols) || (grp == 2 && !cout)) return 0;
   const int64_t nc = d->nchunk;
   int cpw = 0;
   for (int c : {1, 2, 4, 8})
@@ -494,16 +510,18 @@ int sglq_gemv_row_grouped(const sglq_dev *d, const void *const *codes_e,
   a.codes_e = (const u32x4_t *const *)codes_e;
   a.meta_e = meta_e;
   a.ids = ids;
-  a.nid = k;
+  a.nid = npairs;
+  a.slots = slots;
   a.nexp = nexp;
   a.lda = lda;
   a.ldc = ldc;
+  a.ldo = ldo;
   a.kcols = kcols;
   a.cw = cw;
   a.cout = cout;
   a.cnt = d->gv_cnt;
   const int tpg = 8 >> ksl;
-  const dim3 grid((unsigned)((d->ntile + tpg - 1) / tpg), (unsigned)k);
+  const dim3 grid((unsigned)((d->ntile + tpg - 1) / tpg), (unsigned)npairs);
   const int np = dt == SGLQ_DT_BF16 && grp == 1 ? 1 : 2;
   const int spc = d->kind == SGLQ_KIND_U8 ? 2 : 4;
   const size_t lds = (size_t)8 * np * (cpw * spc * 4 + 4) * 16;

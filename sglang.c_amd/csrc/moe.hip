@@ -218,10 +218,16 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
         T <= 4 && sglq_gemv_grouped_fits(g0, T, split1) && sglq_gemv_grouped_fits(d0, T, 1);
     const bool fuse = !decode && sglq_gemm_lds_direct(g0) && mi % 16 == 0;
     int *rowmax = fuse ? (int *)(ws + o_rmax) : nullptr;
-    // one token whose grouped GEMVs can read its routing directly (slot j = segment j): no
-    // routing kernel (DeepSeek MoE decode, T = 1: one launch of ~2-4 us fewer)
-    const bool direct = decode && T == 1 &&
-                        sglq_moe_direct_ok(g0, d0, h, h_dtype, E, gu, k, mi);
+    // one-token decode whose grouped GEMVs read the routing directly (slot j is its own
+    // one-row segment): no routing kernel, on the one-row kernel where the weights allow, else
+    // on the grouped wave-staged kernel.  DeepSeek MoE decode T = 1: 20.0 -> 15.5 us with the
+    // fast silu.  Four tokens as 24 one-row pairs (experts two tokens share read twice)
+    // measured slower than routed segments on the wave-staged kernel (46.7 against 39.8 us).
+    const bool rowdirect = decode && T == 1 &&
+                           sglq_gemv_row_grouped_ok(g0, 1, h, h_dtype, E, 0) &&
+                           sglq_gemv_row_grouped_ok(d0, 2, gu, SGLQ_DT_F32, 2 * mi, (int)mi);
+    const bool direct =
+        rowdirect || (decode && T == 1 && sglq_moe_direct_ok(g0, d0, h, h_dtype, E, gu, k, mi));
     if (!direct) {
       k_moe_route<<<1, 1024, 0, st>>>(topk_ids, (int)P, k, n_exp, SGLQ_MOE_BM, rowmap, pos,
                                       segs, nseg, rowmax);
@@ -243,20 +249,22 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
       // one token read straight from its routing: the one-row kernel where the weights allow
       // (f16 group scales, one group per chunk), else the grouped wave-staged kernel
       int r1 = 0, r2 = 0;
-      if (direct) {
-        r1 = sglq_gemv_row_grouped(g0, g1.codes, g1.meta, topk_ids, (int)k, n_exp, 1, h,
-                                   h_dtype, E, 0, gu, 2 * mi, nullptr, nullptr, st);
-        if (r1 < 0) return -1;
+      if (rowdirect) {
+        r1 = sglq_gemv_row_grouped(g0, g1.codes, g1.meta, topk_ids, (int)P, (int)k, n_exp, 1,
+                                   h, h_dtype, E, 0, gu, 2 * mi, nullptr, nullptr, 0, st);
+        r2 = r1 < 0 ? -1
+                    : sglq_gemv_row_grouped(d0, g2.codes, g2.meta, topk_ids, (int)P, (int)k,
+                                            n_exp, 2, gu, SGLQ_DT_F32, 2 * mi, (int)mi, o, E,
+                                            topk_w, out, E, st);
+        if (r1 != 1 || r2 != 1) {
+          sglq_log_error("qmoe: grouped one-row decode launch failed");
+          return -1;
+        }
+        combined = 1;
       }
       if (!r1 && sglq_gemv_grouped(g0, &g1, T, max_segs, h, h_dtype, T, E, 1, rowmap, 0, gu,
                                    2 * mi, st) != 0)
         return -1;
-      if (direct) {
-        r2 = sglq_gemv_row_grouped(d0, g2.codes, g2.meta, topk_ids, (int)k, n_exp, 2, gu,
-                                   SGLQ_DT_F32, 2 * mi, (int)mi, o, E, topk_w, out, st);
-        if (r2 < 0) return -1;
-        combined = r2;
-      }
       // one token: the down launch also does the combine when it can
       const sglq_combine cb = {pos, topk_w, k, out, &combined};
       if (!r2 && sglq_gemv_grouped(d0, &g2, T, max_segs, gu, SGLQ_DT_F32, P, 2 * mi, 2, nullptr,

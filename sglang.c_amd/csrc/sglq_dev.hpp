@@ -105,14 +105,19 @@ int sglq_gemv(sglq_dev *d, const void *A, int dt, int64_t lda, int64_t M, const 
 // (the caller takes sglq_gemv), -1 = launch error.
 int sglq_gemv_row(const sglq_dev *d, const void *A, int dt, const float *bias, float *C,
                   hipStream_t st);
-// Grouped one-token MoE decode GEMV on the one-row kernel (gemv_row.hip): slot j of the
-// routing (expert ids[j], empty if outside [0, nexp)) writes C row j; grp 1 multiplies the
-// token row A, grp 2 silu(A[j][:K]) * A[j][kcols:] (f32, lda) and also writes cout = the
-// slot-order weighted sum (weights cw) of the rows.  1 = launched, 0 = not applicable, -1 = error.
+// Grouped MoE decode GEMV on the one-row kernel (gemv_row.hip) for npairs = tokens x slots
+// routing pairs read straight from the routing: pair j (expert ids[j], empty if outside
+// [0, nexp)) writes C row j; grp 1 multiplies token row j / slots of A (lda), grp 2
+// silu(A[j][:K]) * A[j][kcols:] (f32, lda) and also writes cout[t] (ldo) = the slot-order
+// weighted sum (weights cw) of token t's rows.  _ok: whether the weights and rows qualify.
+// 1 = launched, 0 = not applicable, -1 = error.
+int sglq_gemv_row_grouped_ok(const sglq_dev *d, int grp, const void *A, int dt, int64_t lda,
+                             int kcols);
 int sglq_gemv_row_grouped(const sglq_dev *d, const void *const *codes_e,
-                          const void *const *meta_e, const int32_t *ids, int k, int nexp,
-                          int grp, const void *A, int dt, int64_t lda, int kcols, float *C,
-                          int64_t ldc, const float *cw, float *cout, hipStream_t st);
+                          const void *const *meta_e, const int32_t *ids, int npairs, int slots,
+                          int nexp, int grp, const void *A, int dt, int64_t lda, int kcols,
+                          float *C, int64_t ldc, const float *cw, float *cout, int64_t ldo,
+                          hipStream_t st);
 // Kernels behind the host-buffer entry points (int8.hip), launched on st.
 int sglq_launch_quant_rows_i8(const float *x, int8_t *q, float *scales, int64_t rows,
                               int64_t dim, hipStream_t st);
