@@ -314,6 +314,7 @@ struct GemmArgs {
   float *part;    // k_gemm_lds split over K: unscaled partial sums [gridDim.y][M][N], else null
   int swiglu;     // k_gemm_lds grouped: mi > 0 = C gets silu(gate) * up, [rows][mi] (see there)
   int *rowmax;    // with swiglu: per row, bits of the largest |C| (atomic max, preset to 0)
+  int epi;        // k_gemm_breg: 1 = whole-row epilogue through LDS, 0 = per-lane stores
 };
 
 union H8 {
@@ -976,6 +977,15 @@ __global__ __launch_bounds__(128 * WMW, 2) void k_gemm_lds(GemmArgs a) {
   lds_epilogue<MB, TN, NT16, E2M1>(a, acc, m0 + wm * (16 * MB), mend, bn, wn, colexp, n16, kq);
 }
 
+template <int MBW, int TN, bool E2M1, int RP, int WN>
+__device__ void wide_epilogue(const GemmArgs &a, const float4_t (&acc)[MBW][TN], float *stg,
+                              int m0, int mend, int bn, int w, int n16, int kq,
+                              const uint8_t *colexp);
+template <int MBW, int TN, bool E2M1, int RP, int WN>
+__device__ void swiglu_epilogue(const GemmArgs &a, const float4_t (&acc)[MBW][TN], float *stg,
+                                int m0, int mend, int bn, int w, int n16, int kq,
+                                const uint8_t *colexp);
+
 // Prefill GEMM for row blocks of at most 64 rows (dense M <= 64, MoE expert blocks) on the
 // direct formats: the same 64 x 128 tile, operands and epilogue as k_gemm_lds<.., 128, .., 1,
 // .., 4, ..>, but each weight tile feeds a single wave there, so a trip through LDS buys no
@@ -1153,6 +1163,17 @@ __global__ __launch_bounds__(64 * WN, 2) void k_gemm_breg(GemmArgs a) {
       }
     }
   }
+  if (a.epi) {  // whole rows through LDS (the A buffers are free after the loop's barrier)
+    constexpr int COLS = 16 * NT16, RP = 16;
+    static_assert(RP * COLS * 4 <= 2 * AITEMS * 16, "k_gemm_breg: epilogue staging");
+    if (a.swiglu)
+      swiglu_epilogue<MB, TN, E2M1, RP, WN>(a, acc, (float *)s_a, m0, mend, bn, wn, n16, kq,
+                                            colexp);
+    else
+      wide_epilogue<MB, TN, E2M1, RP, WN>(a, acc, (float *)s_a, m0, mend, bn, wn, n16, kq,
+                                          colexp);
+    return;
+  }
   lds_epilogue<MB, TN, NT16, E2M1>(a, acc, m0, mend, bn, wn, colexp, n16, kq);
 }
 
@@ -1162,9 +1183,9 @@ __global__ __launch_bounds__(64 * WN, 2) void k_gemm_breg(GemmArgs a) {
 // 2^(rowexp[m] + ce[n]) acc + bias[n]; partials are stored unscaled.  stg: at least
 // RP x 64 TN floats of LDS, free for this use (every wave is past its last LDS read).
 template <int MBW, int TN, bool E2M1, int RP, int WN>
-__device__ __forceinline__ void wide_epilogue(const GemmArgs &a, const float4_t (&acc)[MBW][TN],
-                                              float *stg, int m0, int bn, int w, int n16,
-                                              int kq) {
+__device__ void wide_epilogue(const GemmArgs &a, const float4_t (&acc)[MBW][TN], float *stg,
+                              int m0, int mend, int bn, int w, int n16, int kq,
+                              const uint8_t *colexp) {
   // wave w holds every 16-row block i < MBW of column group w; pass (i, h) stages rows
   // h RP .. h RP + RP - 1 of block i
   constexpr int COLS = 16 * WN * TN, C4 = COLS / 4, ITEMS = RP * C4, NTH = 64 * WN;
@@ -1189,14 +1210,14 @@ __device__ __forceinline__ void wide_epilogue(const GemmArgs &a, const float4_t 
       for (int e = tid; e < ITEMS; e += NTH) {
         const int row = e / C4, c4 = e % C4;
         const int m = m0 + 16 * i + h * RP + row, n = nb + 4 * c4;
-        if (m >= a.M || n >= a.N) continue;
+        if (m >= mend || n >= a.N) continue;
         float4_t v = *(const float4_t *)(stg + row * COLS + 4 * c4);
         if (!a.part) {
           const int re = a.rowexp[m];
 #pragma unroll
           for (int u = 0; u < 4; u++) {
             const int nn = min(n + u, a.N - 1);
-            const int ce = E2M1 ? (int)a.colexp[nn] - 127 : 0;
+            const int ce = E2M1 ? (int)colexp[nn] - 127 : 0;
             v[u] = ldexpf(v[u], re + ce) + (a.bias ? a.bias[nn] : 0.f);
           }
         }
@@ -1210,6 +1231,77 @@ __device__ __forceinline__ void wide_epilogue(const GemmArgs &a, const float4_t 
         }
       }
       __syncthreads();
+    }
+  }
+}
+
+// Epilogue of the grouped gate/up launch (MoE, k_gemm_breg with the SwiGLU): wave w's tile
+// pairs (2p, 2p + 1) hold gate tile g and up tile g + mi / 16 of the same columns, so
+// silu(g) * u is formed in registers (reference src/deepseek.c:662-663), staged through LDS RP
+// rows at a time and stored as whole rows of C [rows][mi]; the row maxima of |C| go to
+// a.rowmax (one atomic max per row and wave) for the next prep.
+template <int MBW, int TN, bool E2M1, int RP, int WN>
+__device__ void swiglu_epilogue(const GemmArgs &a, const float4_t (&acc)[MBW][TN], float *stg,
+                                int m0, int mend, int bn, int w, int n16, int kq,
+                                const uint8_t *colexp) {
+  constexpr int HC = 8 * WN * TN, C4 = HC / 4, ITEMS = RP * C4, NTH = 64 * WN;
+  const int tid = threadIdx.x, mi = a.swiglu, nb = bn * HC;
+  const bool vec = ((uintptr_t)a.C % 16 == 0) && (a.ldc % 4 == 0) && (mi % 4 == 0);
+  float rmx[MBW][4];
+#pragma unroll
+  for (int i = 0; i < MBW; i++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) rmx[i][r] = 0.f;
+#pragma unroll
+  for (int i = 0; i < MBW; i++) {
+#pragma unroll
+    for (int h = 0; h < 16 / RP; h++) {
+#pragma unroll
+      for (int pj = 0; pj < TN / 2; pj++) {
+        const int col = (w * (TN / 2) + pj) * 16 + n16, n = nb + col;
+        const int ceg = E2M1 ? (int)colexp[min(n, mi - 1)] - 127 : 0;
+        const int ceu = E2M1 ? (int)colexp[min(n, mi - 1) + mi] - 127 : 0;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int row = 4 * kq + r - h * RP, m = m0 + 16 * i + 4 * kq + r;
+          if (row < 0 || row >= RP) continue;
+          float v = 0.f;
+          if (n < mi && m < mend) {
+            const float g = ldexpf(acc[i][2 * pj][r], a.rowexp[m] + ceg);
+            const float u = ldexpf(acc[i][2 * pj + 1][r], a.rowexp[m] + ceu);
+            v = sglq_silu(g) * u;
+          }
+          stg[row * HC + col] = v;
+          rmx[i][r] = fmaxf(rmx[i][r], fabsf(v));
+        }
+      }
+      __syncthreads();
+      for (int e = tid; e < ITEMS; e += NTH) {
+        const int row = e / C4, c4 = e % C4;
+        const int m = m0 + 16 * i + h * RP + row, n = nb + 4 * c4;
+        if (m >= mend || n >= mi) continue;
+        const float4_t v = *(const float4_t *)(stg + row * HC + 4 * c4);
+        float *o = a.C + (int64_t)m * a.ldc + n;
+        if (vec) {
+          *(float4_t *)o = v;
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; u++)
+            if (n + u < mi) o[u] = v[u];
+        }
+      }
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MBW; i++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float x = rmx[i][r];
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));  // the row's 16 lanes
+      const int m = m0 + 16 * i + 4 * kq + r;
+      if (n16 == 0 && m < mend) atomicMax(&a.rowmax[m], __float_as_int(x));
     }
   }
 }
@@ -1434,7 +1526,8 @@ __global__ __launch_bounds__(64 * WN, 1) void k_gemm_dma(GemmArgs a) {
   constexpr int RP = 16 * 16 * NT16 * 4 <= AITEMS * 16 ? 16
                      : 8 * 16 * NT16 * 4 <= AITEMS * 16 ? 8 : 4;
   static_assert(RP * 16 * NT16 * 4 <= AITEMS * 16, "k_gemm_dma: epilogue staging");
-  wide_epilogue<MBW, TN, E2M1, RP, WN>(a, acc, (float *)sA0, m0, bn, w, n16, kq);
+  wide_epilogue<MBW, TN, E2M1, RP, WN>(a, acc, (float *)sA0, m0, mend, bn, w, n16, kq,
+                                       a.colexp);
 }
 
 // Sum of the K-split partials of k_gemm_lds in slice order (deterministic), then the row and
@@ -1851,6 +1944,12 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
     }
     const dim3 grid2(gx, (unsigned)pl.nz);
     if (grp) {  // expert row blocks of at most 64 rows: codes unpacked in registers
+      static int epi = -1;
+      if (epi < 0) {
+        const char *e = getenv("SGLQ_BREG_EPI");  // 0: per-lane stores (A/B measurement)
+        epi = e ? atoi(e) : 1;
+      }
+      a.epi = epi;
       switch (d->kind) {
         case SGLQ_KIND_U4:
           if (split) launch_breg<SGLQ_KIND_U4, 2>(a, grid2, st);
