@@ -58,7 +58,7 @@ typedef __attribute__((address_space(1))) const u32x4_t GU4;
 
 template <int KIND, int CPW, int TPW, int DT, bool SCF16, bool MV, int NW, int GRP = 0>
 __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
-  static_assert(GRP != 2 || DT == SGLQ_DT_F32, "SwiGLU rows are f32");
+  static_assert(GRP < 2 || DT == SGLQ_DT_F32, "SwiGLU rows are f32");
   static_assert(GRP == 0 || (TPW == 1 && KIND != SGLQ_KIND_E2M1), "grouped: one tile per wave");
   constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
   constexpr int NP = DT == SGLQ_DT_BF16 ? 1 : 2;     // f16 operand rows: hi (+ lo)
@@ -73,13 +73,28 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
   const int lane = (int)threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int ks = 1 << a.ksl;
-  const int tg = (int)blockIdx.x * (NW >> a.ksl) + (w >> a.ksl);  // tile group
+  // GRP 3: one tile per workgroup, wave w = (routing slot w >> ksl, K slice); otherwise
+  // wave w >> ksl takes tile group blockIdx.x * (NW >> ksl) + (w >> ksl)
+  const int tg = GRP == 3 ? (int)blockIdx.x : (int)blockIdx.x * (NW >> a.ksl) + (w >> a.ksl);
   const int t0 = tg * TPW;                                        // its first tile
   const int sl = w & (ks - 1);
   const int c0 = sl * CPW;
+  // GRP 3: this wave's slot and whether it is routed (an empty slot's waves stream the first
+  // routed expert's chunk 0 and contribute zero)
+  int slot = 0, e3 = -1, e3first = -1;
+  if constexpr (GRP == 3) {
+    slot = w >> a.ksl;
+    for (int j = 0; j < a.nid; j++) {
+      const bool v = a.ids[j] >= 0 && a.ids[j] < a.nexp;
+      if (v && e3first < 0) e3first = a.ids[j];
+      if (j == slot && v) e3 = a.ids[j];
+    }
+  }
   // chunks of this wave (0 for a wave past the last tile or chunk: it streams chunk 0 of the
   // last tile and contributes zero)
-  const int nch = t0 < a.ntile && c0 < a.nchunk ? min(CPW, a.nchunk - c0) : 0;
+  const int nch = t0 < a.ntile && c0 < a.nchunk && (GRP != 3 || e3 >= 0)
+                      ? min(CPW, a.nchunk - c0)
+                      : 0;
   const int cb = nch > 0 ? c0 : 0;
   const int n16 = lane & 15, kq = lane >> 4;
   // grouped: this workgroup's routing slot and its expert's weights
@@ -88,7 +103,17 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
   const char *arow = (const char *)a.A;
   float *crow = a.C;
   int ns = 0;
-  if constexpr (GRP != 0) {
+  if constexpr (GRP == 3) {
+    if (e3first < 0) {  // no routed slot: the combined row is zero
+      const int n = t0 * 16 + n16;
+      if (w == 0 && kq == 0 && t0 < a.ntile && n < a.N) a.cout[n] = 0.f;
+      return;
+    }
+    const int e = e3 >= 0 ? e3 : e3first;
+    codes = a.codes_e[e];
+    meta = a.meta_e[e];
+    arow += (int64_t)slot * a.lda * 4;
+  } else if constexpr (GRP != 0) {
     for (int j = 0; j < a.nid; j++) ns += a.ids[j] >= 0 && a.ids[j] < a.nexp;
     const int y = (int)blockIdx.y, e = y < a.nid ? a.ids[y] : -1;
     if (GRP == 2 && ns == 0) {  // no routed pair: the combined rows are zero
@@ -117,7 +142,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
 
   // ---- loads: activations, meta, codes (all issued before any is used)
   constexpr int RW = DT == SGLQ_DT_F32 ? 2 : 1;  // 128-bit words per 8-element item
-  constexpr int RU = GRP == 2 ? RW : 0;          // and as many of the up half (SwiGLU rows)
+  constexpr int RU = GRP >= 2 ? RW : 0;          // and as many of the up half (SwiGLU rows)
   u32x4_t raw[NQ][RW + RU];
 #pragma unroll
   for (int q = 0; q < NQ; q++) {
@@ -129,7 +154,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
     const GU4 *p = ok ? (const GU4 *)(arow + (int64_t)k * (RW * 2)) : (const GU4 *)g_zero_item;
 #pragma unroll
     for (int i = 0; i < RW; i++) raw[q][i] = p[i];
-    if constexpr (GRP == 2) {
+    if constexpr (GRP >= 2) {
       const GU4 *pu = ok ? (const GU4 *)(arow + ((int64_t)a.kcols + k) * 4)
                          : (const GU4 *)g_zero_item;
 #pragma unroll
@@ -196,7 +221,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
   auto decode = [&](int q, float (&v)[8]) {
 #pragma unroll
     for (int o = 0; o < 8; o++) {
-      if constexpr (GRP == 2)  // silu(gate) * up (reference src/deepseek.c:662-663)
+      if constexpr (GRP >= 2)  // silu(gate) * up (reference src/deepseek.c:662-663)
         v[o] = sglq_silu(__uint_as_float(raw[q][o >> 2][o & 3])) *
                __uint_as_float(raw[q][RW + (o >> 2)][o & 3]);
       else if constexpr (DT == SGLQ_DT_F32)
@@ -322,6 +347,23 @@ __global__ __launch_bounds__(NW * 64) void k_gemv_row(RowArgs a) {
     }
   }
 
+  if constexpr (GRP == 3) {
+    // every slot's slices, then out[n] = ((0 + w0 o0) + w1 o1) + ... in slot order, each o the
+    // slot's slices added in slice order, as k_moe_combine (reference src/deepseek.c:675-676)
+    if (kq == 0) s_sum[w][0][n16] = f[0];
+    __syncthreads();
+    const int n = t0 * 16 + n16;
+    if (w != 0 || kq != 0 || t0 >= a.ntile || n >= a.N) return;
+    float out = 0.f;
+    for (int j = 0; j < a.nid && j < (NW >> a.ksl); j++) {
+      if (a.ids[j] < 0 || a.ids[j] >= a.nexp) continue;
+      float o = s_sum[j << a.ksl][0][n16];
+      for (int q = 1; q < ks; q++) o += s_sum[(j << a.ksl) + q][0][n16];
+      out = __fadd_rn(out, __fmul_rn(a.cw[j], o));
+    }
+    a.cout[n] = out;
+    return;
+  }
   // ---- K slices of a tile group added in slice order, then bias and store (lanes 0-15)
   if (ks > 1) {
     if (kq == 0) {
@@ -454,9 +496,33 @@ bool launch_row_grp2(const RowArgs &a, int cpw, dim3 grid, size_t lds, hipStream
     default: return false;
   }
 }
+// GRP 3: 16 waves, up to 8 slots x 2 K slices of one tile
+template <int KIND, int C, bool MV>
+void launch_row_grp3c(const RowArgs &a, dim3 grid, size_t lds, hipStream_t st) {
+  auto f = k_gemv_row<KIND, C, 1, SGLQ_DT_F32, true, MV, 16, 3>;
+  // dynamic LDS beyond 64 KiB is enabled per kernel; the request must leave room for the
+  // kernel's static LDS (the slice sums) within the 160 KiB of a workgroup
+  static size_t raised = 0;
+  if (lds > 64 * 1024 && lds > raised &&
+      hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)lds) == hipSuccess)
+    raised = lds;
+  f<<<grid, 1024, lds, st>>>(a);
+}
+template <int KIND>
+bool launch_row_grp3(const RowArgs &a, int cpw, dim3 grid, size_t lds, hipStream_t st) {
+  switch (cpw) {
+    case 1: launch_row_grp3c<KIND, 1, false>(a, grid, lds, st); return true;
+    case 2: launch_row_grp3c<KIND, 2, false>(a, grid, lds, st); return true;
+    case 4: launch_row_grp3c<KIND, 4, true>(a, grid, lds, st); return true;
+    case 8: launch_row_grp3c<KIND, 8, true>(a, grid, lds, st); return true;
+    default: return false;
+  }
+}
 template <int KIND>
 bool launch_row_grp(const RowArgs &a, int grp, int dt, int cpw, dim3 grid, size_t lds,
                     hipStream_t st) {
+  if (grp == 3) return launch_row_grp3<KIND>(a, cpw, grid, lds, st);
   if (grp == 2) return launch_row_grp2<KIND, 2, SGLQ_DT_F32>(a, cpw, grid, lds, st);
   if (dt == SGLQ_DT_F32) return launch_row_grp2<KIND, 1, SGLQ_DT_F32>(a, cpw, grid, lds, st);
   if (dt == SGLQ_DT_F16) return launch_row_grp2<KIND, 1, SGLQ_DT_F16>(a, cpw, grid, lds, st);
@@ -487,14 +553,20 @@ int sglq_gemv_row_grouped(const sglq_dev *d, const void *const *codes_e,
                           int nexp, int grp, const void *A, int dt, int64_t lda, int kcols,
                           float *C, int64_t ldc, const float *cw, float *cout, int64_t ldo,
                           hipStream_t st) {
-  if (!sglq_gemv_row_grouped_ok(d, grp, A, dt, lda, kcols) || (grp == 2 && !cout)) return 0;
+  if (!sglq_gemv_row_grouped_ok(d, grp == 3 ? 2 : grp, A, dt, lda, kcols) ||
+      (grp >= 2 && !cout))
+    return 0;
   const int64_t nc = d->nchunk;
+  // grp 3 (one token, at most 8 slots, K within two slices of 8 chunks): two K slices per slot
+  if (grp == 3 && (npairs > 8 || npairs != slots || nc > 16)) return 0;
+  const int ways = grp == 3 ? 2 : 8;  // K slices per workgroup row of waves
   int cpw = 0;
   for (int c : {1, 2, 4, 8})
-    if (!cpw && 8 * c >= nc) cpw = c;
+    if (!cpw && ways * c >= nc) cpw = c;
   if (!cpw) return 0;
   int ksl = 0;
-  while ((1 << ksl) * cpw < nc && (2 << ksl) <= 8) ksl++;
+  while ((1 << ksl) * cpw < nc && (2 << ksl) <= ways) ksl++;
+  if (grp == 3) ksl = 1;
   RowArgs a;
   memset(&a, 0, sizeof(a));
   a.A = A;
@@ -520,11 +592,11 @@ int sglq_gemv_row_grouped(const sglq_dev *d, const void *const *codes_e,
   a.cw = cw;
   a.cout = cout;
   a.cnt = d->gv_cnt;
-  const int tpg = 8 >> ksl;
-  const dim3 grid((unsigned)((d->ntile + tpg - 1) / tpg), (unsigned)npairs);
+  const int tpg = grp == 3 ? 1 : 8 >> ksl;
+  const dim3 grid((unsigned)((d->ntile + tpg - 1) / tpg), grp == 3 ? 1u : (unsigned)npairs);
   const int np = dt == SGLQ_DT_BF16 && grp == 1 ? 1 : 2;
   const int spc = d->kind == SGLQ_KIND_U8 ? 2 : 4;
-  const size_t lds = (size_t)8 * np * (cpw * spc * 4 + 4) * 16;
+  const size_t lds = (size_t)(grp == 3 ? 16 : 8) * np * (cpw * spc * 4 + 4) * 16;
   const bool ok = d->kind == SGLQ_KIND_U8
                       ? launch_row_grp<SGLQ_KIND_U8>(a, grp, dt, cpw, grid, lds, st)
                       : launch_row_grp<SGLQ_KIND_U4>(a, grp, dt, cpw, grid, lds, st);

@@ -252,10 +252,15 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
       if (rowdirect) {
         r1 = sglq_gemv_row_grouped(g0, g1.codes, g1.meta, topk_ids, (int)P, (int)k, n_exp, 1,
                                    h, h_dtype, E, 0, gu, 2 * mi, nullptr, nullptr, 0, st);
+        // down: one workgroup per output tile holding every slot (combine through LDS), else
+        // one per (slot, tile) with the combine done by the last slot of each tile
         r2 = r1 < 0 ? -1
                     : sglq_gemv_row_grouped(d0, g2.codes, g2.meta, topk_ids, (int)P, (int)k,
-                                            n_exp, 2, gu, SGLQ_DT_F32, 2 * mi, (int)mi, o, E,
+                                            n_exp, 3, gu, SGLQ_DT_F32, 2 * mi, (int)mi, o, E,
                                             topk_w, out, E, st);
+        if (r2 == 0)
+          r2 = sglq_gemv_row_grouped(d0, g2.codes, g2.meta, topk_ids, (int)P, (int)k, n_exp, 2,
+                                     gu, SGLQ_DT_F32, 2 * mi, (int)mi, o, E, topk_w, out, E, st);
         if (r1 != 1 || r2 != 1) {
           sglq_log_error("qmoe: grouped one-row decode launch failed");
           return -1;

@@ -109,7 +109,9 @@ int sglq_gemv_row(const sglq_dev *d, const void *A, int dt, const float *bias, f
 // routing pairs read straight from the routing: pair j (expert ids[j], empty if outside
 // [0, nexp)) writes C row j; grp 1 multiplies token row j / slots of A (lda), grp 2
 // silu(A[j][:K]) * A[j][kcols:] (f32, lda) and also writes cout[t] (ldo) = the slot-order
-// weighted sum (weights cw) of token t's rows.  _ok: whether the weights and rows qualify.
+// weighted sum (weights cw) of token t's rows; grp 3 (one token, at most 8 slots) writes only
+// cout, combining the slots inside each tile's workgroup.  _ok: whether the weights and rows
+// qualify.
 // 1 = launched, 0 = not applicable, -1 = error.
 int sglq_gemv_row_grouped_ok(const sglq_dev *d, int grp, const void *A, int dt, int64_t lda,
                              int kcols);
