@@ -564,6 +564,10 @@ int sglq_gemv_row_grouped(const sglq_dev *d, const void *const *codes_e,
   for (int c : {1, 2, 4, 8})
     if (!cpw && ways * c >= nc) cpw = c;
   if (!cpw) return 0;
+  if (const char *ov = getenv("SGLQ_ROW_PLAN")) {  // "cpw,..." (measurement override, grp 1)
+    const int c = atoi(ov);
+    if (grp == 1 && (c == 1 || c == 2 || c == 4 || c == 8) && ways * c >= nc) cpw = c;
+  }
   int ksl = 0;
   while ((1 << ksl) * cpw < nc && (2 << ksl) <= ways) ksl++;
   if (grp == 3) ksl = 1;
