@@ -299,12 +299,13 @@ def ceilings(torch, warmup):
         slice16 = kb * 1024 // 16
         buf = torch.ones(256 * slice16 * 4, dtype=torch.int32, device="cuda")
         iters = max(1, (64 << 20) // (256 * slice16 * 16)) * 4
-        for u in (8, 16):
+        for u in (8, 16, -8, -16):
             t = time_graph(torch, lambda: lib.sglc_l2_read(
                 C.c_void_p(buf.data_ptr()), 256, slice16, iters, u,
                 C.c_void_p(sink.data_ptr()), st()), REPLAYS, warmup)
             nb = 256 * slice16 * 16 * iters
-            res[f"cu_read_{kb}KiB_per_cu_u{u}"] = {"TB/s": round(nb / t / 1e12, 2),
+            tag = f"u{u}" if u > 0 else f"lds_dma_u{-u}"
+            res[f"cu_read_{kb}KiB_per_cu_{tag}"] = {"TB/s": round(nb / t / 1e12, 2),
                                                     "GB/s_per_cu": round(nb / t / 1e9 / 256, 1)}
         del buf
     import synth

@@ -51,6 +51,29 @@ __global__ __launch_bounds__(256) void k_l2_read(const u4_t *__restrict__ p, int
   if (x == 0x9E3779B9u) sink[blockIdx.x & 1023] = x;
 }
 
+// The same per-CU intake through global_load_lds_dwordx4 (data lands in LDS, no registers):
+// U copies of 16 bytes per thread in flight into a ring of LDS buffers, then a wait.
+template <int U>
+__global__ __launch_bounds__(256) void k_l2_read_lds(const u4_t *__restrict__ p, int slice16,
+                                                     int iters, uint32_t *__restrict__ sink) {
+  __shared__ u4_t buf[U * 256];  // U x 4 KiB
+  const u4_t *q = p + (int64_t)blockIdx.x * slice16;
+  const int w = threadIdx.x >> 6;
+  for (int it = 0; it < iters; it++) {
+    for (int b = 0; b < slice16; b += 256 * U) {
+#pragma unroll
+      for (int u = 0; u < U; u++)
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void *)(q + (b + u * 256 + threadIdx.x) % slice16),
+            (__attribute__((address_space(3))) void *)(buf + u * 256 + 64 * w), 16, 0, 0);
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+  }
+  __syncthreads();
+  const uint32_t x = buf[threadIdx.x].x ^ buf[(threadIdx.x + 7) % (U * 256)].y;
+  if (x == 0x9E3779B9u) sink[blockIdx.x & 1023] = x;
+}
+
 __global__ void k_empty() {}
 
 // MFMA issue loops: every wave runs `iters` x 8 independent accumulation chains.  Operands come
@@ -273,15 +296,20 @@ __attribute__((visibility("default"))) int sglc_mfma_valu(int nv, int grid, int 
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// L2-resident read stream (k_l2_read): bytes read = grid * slice16 * 16 * iters.
+// L2-resident read stream (k_l2_read; u = -8 / -16: k_l2_read_lds): bytes read =
+// grid * slice16 * 16 * iters.
 __attribute__((visibility("default"))) int sglc_l2_read(const void *p, int grid, int slice16,
                                                          int iters, int u, uint32_t *sink,
                                                          void *stream) {
   hipStream_t st = (hipStream_t)stream;
   if (u == 16)
     k_l2_read<16><<<grid, 256, 0, st>>>((const u4_t *)p, slice16, iters, sink);
-  else
+  else if (u == 8)
     k_l2_read<8><<<grid, 256, 0, st>>>((const u4_t *)p, slice16, iters, sink);
+  else if (u == -16)  // negative u: the global_load_lds form
+    k_l2_read_lds<16><<<grid, 256, 0, st>>>((const u4_t *)p, slice16, iters, sink);
+  else
+    k_l2_read_lds<8><<<grid, 256, 0, st>>>((const u4_t *)p, slice16, iters, sink);
   return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
