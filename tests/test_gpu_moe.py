@@ -113,3 +113,19 @@ def test_moe_decode_one_token(orc, fmt):
     _check(orc, 8, 512, 256, 1, 3, seed=91, fmt=fmt)
     _check(orc, 6, 256, 384, 1, 4, seed=93, fmt=fmt, dtypes=("f32",), drop=True)
     _check(orc, 4, 256, 128, 1, 2, seed=95, fmt=fmt, dtypes=("bf16",), drop="all")
+
+
+def test_moe_decode_one_token_many_slots(orc):
+    """One token routed to 10 experts: more slots than the in-workgroup combine holds (8), so
+    the down launch keeps one workgroup per (tile, slot) and the last slot of each tile
+    combines; with and without unrouted slots."""
+    _check(orc, 16, 256, 128, 1, 10, seed=97)
+    _check(orc, 16, 256, 128, 1, 10, seed=98, dtypes=("f32",), drop=True)
+
+
+def test_moe_decode_one_token_u8_g64(orc):
+    """One token over 8-bit experts with 64-element groups (one group per 64-element chunk):
+    both launches take the grouped one-row kernel's 8-bit form."""
+    _check(orc, 8, 512, 256, 1, 4, seed=99, fmt="gptq8_g64")
+    _check(orc, 8, 512, 256, 1, 4, seed=100, fmt="gptq8_g64", dtypes=("f32",), drop=True)
+
