@@ -286,11 +286,21 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
       if (sglq_gemm_run(g0, &g1, ws + o_aop1, (const int *)(ws + o_rexp1), P, Mpad, maxblk,
                         split1, nullptr, gu, mi, nullptr, st) != 0)
         return -1;
-      if (sglq_prep_a(d0, 0, gu, SGLQ_DT_F32, mi, P, Mpad, nullptr, 0, 1, ws + o_aop2,
+      // the down operands silu(g) * u (f32) as one f16 piece under the row's power of two (a
+      // 2^-12 relative rounding, as the prescaled weights'): half the MFMAs and operand bytes
+      // of the hi + lo split.  Config 5 prefill 199 -> 174 us; max rel error against the
+      // reference 3.2e-4 -> 3.9e-4 (at most 5.2e-4 over the MoE tests; bar 1e-3).
+      // SGLQ_MOE_DOWN_SPLIT=1 keeps hi + lo.
+      static int dsplit = -1;
+      if (dsplit < 0) {
+        const char *e = getenv("SGLQ_MOE_DOWN_SPLIT");
+        dsplit = e ? atoi(e) : 0;
+      }
+      if (sglq_prep_a(d0, 0, gu, SGLQ_DT_F32, mi, P, Mpad, nullptr, 0, dsplit, ws + o_aop2,
                       (int *)(ws + o_rexp2), st, rowmax) != 0)
         return -1;
-      if (sglq_gemm_run(d0, &g2, ws + o_aop2, (const int *)(ws + o_rexp2), P, Mpad, maxblk, 1,
-                        nullptr, o, E, nullptr, st) != 0)
+      if (sglq_gemm_run(d0, &g2, ws + o_aop2, (const int *)(ws + o_rexp2), P, Mpad, maxblk,
+                        dsplit, nullptr, o, E, nullptr, st) != 0)
         return -1;
     } else {
       // rows of Mpad beyond P: rowmap entries are never read (prep zeroes rows >= M)

@@ -56,6 +56,7 @@ def _check(orc, n_exp, E, mi, T, k, seed, dtypes=("bf16", "f32"), drop=False, fm
                            torch.from_numpy(wts).cuda()).cpu().numpy()
         ref = orc.moe_ffn(hb, wgu, wdn, ids, wts)
         e = rel_err(y, ref)
+        print(f"[gpu]   max rel err {e:.3e}", flush=True)
         assert e <= TOL, (dt, e)
         y2 = q.qmoe_forward(gu, dn, th, torch.from_numpy(ids).cuda(),
                             torch.from_numpy(wts).cuda()).cpu().numpy()
