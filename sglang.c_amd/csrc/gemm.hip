@@ -1639,12 +1639,20 @@ void launch_dma1(const GemmArgs &a, dim3 grid, hipStream_t st) {
 // shapes of k_gemm_dma: 128 rows x 192 columns (4 waves) or x 384 columns (8 waves); two A
 // pieces (f32 rows) use 64-row tiles, the largest whose four A buffers fit the LDS
 template <int KIND, int NP>
-void launch_dma(const GemmArgs &a, int wn, dim3 grid, hipStream_t st) {
-  constexpr int MB = NP == 1 ? 8 : 4;
-  if (wn == 8)
-    launch_dma1<KIND, NP, 3, MB, 8>(a, grid, st);
-  else
-    launch_dma1<KIND, NP, 3, MB, 4>(a, grid, st);
+void launch_dma(const GemmArgs &a, int mb, int wn, dim3 grid, hipStream_t st) {
+  if constexpr (NP == 1) {
+    if (mb == 4)  // up to 64 rows
+      launch_dma1<KIND, NP, 3, 4, 4>(a, grid, st);
+    else if (wn == 8)
+      launch_dma1<KIND, NP, 3, 8, 8>(a, grid, st);
+    else
+      launch_dma1<KIND, NP, 3, 8, 4>(a, grid, st);
+  } else {
+    if (wn == 8)
+      launch_dma1<KIND, NP, 3, 4, 8>(a, grid, st);
+    else
+      launch_dma1<KIND, NP, 3, 4, 4>(a, grid, st);
+  }
 }
 
 template <int KIND, bool SPLIT, bool SCF16, bool STEPM, bool PS, int MB>
@@ -1805,23 +1813,37 @@ static LdsPlan lds_plan(const sglq_dev *d, int64_t M) {
 }
 
 // k_gemm_dma plan of a dense call.  Taken where it measured faster than k_gemm_lds: K of at
-// most 4096 and enough tiles to give most CUs one workgroup without a split over K (no
-// partial sums).  8 waves (384 columns) when that alone gives 200 tiles, else 4 waves (192
+// most 4096, and either at most 64 rows (below) or enough tiles to give most CUs one
+// workgroup without a split over K (no partial sums).  8 waves (384 columns) when that alone gives 200 tiles, else 4 waves (192
 // columns).  Measured (graph replay, GPTQ int4 g128 [11008, 4096], bf16 rows, incl. the A
 // prep): M = 512 95.5 -> 86.5 us, 1024 175 -> 139 us, 2048 289 -> 274 us.  At K = 11008 and
 // where a split over K is needed it measured slower, so those stay on k_gemm_lds.
 // SGLQ_GEMM_DMA=0 keeps every call on k_gemm_lds (A/B measurement).
 struct WidePlan {
-  int use, mb, wn;  // wn waves along N
+  int use, mb, wn, nz;  // wn waves along N, nz slices of K (partials added by k_splitk_reduce)
 };
 static WidePlan wide_plan(const sglq_dev *d, int64_t M, int np) {
-  WidePlan p = {0, np == 1 ? 8 : 4, 4};
-  static int env = -1;
+  WidePlan p = {0, np == 1 ? 8 : 4, 4, 1};
+  static int env = -1, small = -1;
   if (env < 0) {
     const char *e = getenv("SGLQ_GEMM_DMA");
     env = e ? atoi(e) : 1;
+    const char *s = getenv("SGLQ_GEMM_DMA_SMALL");  // rows 17-64 (A/B measurement)
+    small = s ? atoi(s) : 1;
   }
-  if (!env || !lds_direct(d) || M <= 64 || d->K > 4096) return p;
+  if (!env || !lds_direct(d) || d->K > 4096) return p;
+  if (M <= 64) {
+    // one 64-row block: 192-column tiles with K cut into nz slices for about 232 workgroups.
+    // [11008, 4096] bf16 against k_gemm_lds: M = 25 36.9 -> 32.2 us, 48 39.1 -> 35.4, 64
+    // 40.2 -> 37.3 (A prep and slice sums included); at K = 11008 it measured slower (M = 64
+    // 43.5 -> 54.6), as does every K > 4096 below.
+    if (!small) return p;
+    p.mb = 4;
+    const int64_t tiles = (d->N + 191) / 192;
+    p.nz = (int)std::max<int64_t>(1, std::min<int64_t>(d->nchunk / 4, (256 + tiles / 2) / tiles));
+    p.use = 1;
+    return p;
+  }
   const int64_t bmr = 16 * p.mb, nbm = (M + bmr - 1) / bmr;
   if (nbm * ((d->N + 383) / 384) >= 200) {
     p.use = 1;
@@ -1896,26 +1918,36 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
     const WidePlan wp = wide_plan(d, M, split ? 2 : 1);
     if (wp.use) {
       const int64_t bmr = 16 * wp.mb, cols = 48 * wp.wn;
+      if (wp.nz > 1 && !part) {
+        sglq_log_error("prefill GEMM: no workspace for the split over K");
+        return -1;
+      }
       a.nbm = (int)((M + bmr - 1) / bmr);
       a.nbn = (int)((d->N + cols - 1) / cols);
-      a.part = nullptr;
+      a.part = wp.nz > 1 ? part : nullptr;
       a.xmap = 0;
-      const dim3 grid2((unsigned)(8 * ((a.nbm * a.nbn + 7) / 8)));
+      const dim3 grid2((unsigned)(8 * ((a.nbm * a.nbn + 7) / 8)), (unsigned)wp.nz);
       switch (d->kind) {
         case SGLQ_KIND_U4:
-          if (split) launch_dma<SGLQ_KIND_U4, 2>(a, wp.wn, grid2, st);
-          else launch_dma<SGLQ_KIND_U4, 1>(a, wp.wn, grid2, st);
+          if (split) launch_dma<SGLQ_KIND_U4, 2>(a, wp.mb, wp.wn, grid2, st);
+          else launch_dma<SGLQ_KIND_U4, 1>(a, wp.mb, wp.wn, grid2, st);
           break;
         case SGLQ_KIND_U8:
-          if (split) launch_dma<SGLQ_KIND_U8, 2>(a, wp.wn, grid2, st);
-          else launch_dma<SGLQ_KIND_U8, 1>(a, wp.wn, grid2, st);
+          if (split) launch_dma<SGLQ_KIND_U8, 2>(a, wp.mb, wp.wn, grid2, st);
+          else launch_dma<SGLQ_KIND_U8, 1>(a, wp.mb, wp.wn, grid2, st);
           break;
         default:
-          if (split) launch_dma<SGLQ_KIND_E2M1, 2>(a, wp.wn, grid2, st);
-          else launch_dma<SGLQ_KIND_E2M1, 1>(a, wp.wn, grid2, st);
+          if (split) launch_dma<SGLQ_KIND_E2M1, 2>(a, wp.mb, wp.wn, grid2, st);
+          else launch_dma<SGLQ_KIND_E2M1, 1>(a, wp.mb, wp.wn, grid2, st);
           break;
       }
       SGLQ_HIP(hipGetLastError());
+      if (wp.nz > 1) {
+        k_splitk_reduce<<<dim3((unsigned)((d->N + 255) / 256), (unsigned)M), 256, 0, st>>>(
+            part, wp.nz, (int)M, (int)d->N, rowexp,
+            d->kind == SGLQ_KIND_E2M1 ? d->colexp : nullptr, bias, C, ldc);
+        SGLQ_HIP(hipGetLastError());
+      }
       return 0;
     }
   }
@@ -2020,7 +2052,7 @@ static void gemm_ws_layout(const sglq_dev *d, int dt, int64_t M, int64_t *Mpad_o
   *Mpad_out = Mpad;
   *aop_bytes = sglq_aop_bytes(d, Mpad, split);
   *o_part = (*aop_bytes + (size_t)Mpad * sizeof(int) + 255) / 256 * 256;
-  const int nz = wp.use ? 1 : lds_direct(d) ? lds_plan(d, M).nz : 0;
+  const int nz = wp.use ? wp.nz : lds_direct(d) ? lds_plan(d, M).nz : 0;
   *part_bytes = (size_t)nz * M * d->N * sizeof(float);
 }
 
