@@ -1814,8 +1814,8 @@ static LdsPlan lds_plan(const sglq_dev *d, int64_t M) {
 
 // k_gemm_dma plan of a dense call.  Taken where it measured faster than k_gemm_lds: K of at
 // most 4096, and either at most 64 rows (below) or enough tiles to give most CUs one
-// workgroup without a split over K (no partial sums).  8 waves (384 columns) when that alone gives 200 tiles, else 4 waves (192
-// columns).  Measured (graph replay, GPTQ int4 g128 [11008, 4096], bf16 rows, incl. the A
+// workgroup without a split over K (no partial sums).  8 waves (384 columns) when that
+// alone gives 200 tiles, else 4 waves (192 columns).  Measured (graph replay, GPTQ int4 g128 [11008, 4096], bf16 rows, incl. the A
 // prep): M = 512 95.5 -> 86.5 us, 1024 175 -> 139 us, 2048 289 -> 274 us.  At K = 11008 and
 // where a split over K is needed it measured slower, so those stay on k_gemm_lds.
 // SGLQ_GEMM_DMA=0 keeps every call on k_gemm_lds (A/B measurement).
