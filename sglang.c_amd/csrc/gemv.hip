@@ -302,7 +302,7 @@ __global__ __launch_bounds__(512) void k_gemv(GemvArgs a) {
     if ((int)blockIdx.y >= *a.nseg) return;
     const int4 sg = a.segs[blockIdx.y];
     row0 = sg.y;
-    M = sg.z;
+    M = min(sg.z, a.M);  // the staging holds a.M rows (the host cuts blocks to that)
     codes = a.codes_e[sg.x];
     meta = a.meta_e[sg.x];
   }
@@ -574,7 +574,10 @@ __global__ __launch_bounds__(512) void k_gemv_wave(GemvArgs a) {
     } else {
       ns = *a.nseg;
       live = (int)blockIdx.y < ns;
-      if (live) sg = a.segs[blockIdx.y];
+      if (live) {
+        sg = a.segs[blockIdx.y];
+        sg.z = min(sg.z, min(MR, a.M));  // the staging holds these rows (the host cuts blocks)
+      }
     }
     if (GRP == 2 && a.cout && ns == 0) {
       // no routed slot: the combined row is zero

@@ -17,6 +17,8 @@
 //   k_moe_combine out[t] = sum_j w[t,j] * o[row of (t,j)], slots added in order j = 0..k-1
 #include <string.h>
 
+#include <algorithm>
+
 #include "sglq_dev.hpp"
 
 namespace {
@@ -161,7 +163,12 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
   if (T == 0) return 0;
   {
     const int64_t E = g0->K, mi = d0->K, P = T * k;
-    const int64_t maxblk = (P + SGLQ_MOE_BM - 1) / SGLQ_MOE_BM + n_exp;
+    // row blocks: at most 64 rows of one expert for the grouped GEMMs (at most gblk blocks,
+    // the GEMMs' grid); at most T rows for the decode GEMVs, whose staging holds T rows (a token
+    // that lists an expert twice gives it more rows than there are tokens), so there at most
+    // one block per pair.  maxblk = the table's capacity.
+    const int64_t gblk = (P + SGLQ_MOE_BM - 1) / SGLQ_MOE_BM + n_exp;
+    const int64_t maxblk = std::max<int64_t>(gblk, P);
     const int64_t Mpad = (P + SGLQ_GEMM_BM - 1) / SGLQ_GEMM_BM * SGLQ_GEMM_BM + SGLQ_GEMM_BM;
     const int split1 = h_dtype == SGLQ_DT_F32;
     // workspace (kept in expert 0's gate_up handle)
@@ -229,8 +236,8 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
     const bool direct =
         rowdirect || (decode && T == 1 && sglq_moe_direct_ok(g0, d0, h, h_dtype, E, gu, k, mi));
     if (!direct) {
-      k_moe_route<<<1, 1024, 0, st>>>(topk_ids, (int)P, k, n_exp, SGLQ_MOE_BM, rowmap, pos,
-                                      segs, nseg, rowmax);
+      k_moe_route<<<1, 1024, 0, st>>>(topk_ids, (int)P, k, n_exp, decode ? (int)T : SGLQ_MOE_BM,
+                                      rowmap, pos, segs, nseg, rowmax);
       SGLQ_HIP(hipGetLastError());
     }
     sglq_group g1 = {dp, dp + n_exp, (const uint8_t *const *)(dp + 2 * n_exp), segs, nseg};
@@ -245,7 +252,7 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
     // token rows and the SwiGLU rows directly; otherwise operand prep + grouped GEMMs
     int combined = 0;
     if (decode) {
-      const int64_t max_segs = P < n_exp ? P : n_exp;
+      const int64_t max_segs = P;  // blocks of at most T rows, at least one row each
       // one token read straight from its routing: the one-row kernel where the weights allow
       // (f16 group scales, one group per chunk), else the grouped wave-staged kernel
       int r1 = 0, r2 = 0;
@@ -283,7 +290,7 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
       if (sglq_prep_a(g0, 1, h, h_dtype, E, P, Mpad, rowmap, 0, split1, ws + o_aop1,
                       (int *)(ws + o_rexp1), st) != 0)
         return -1;
-      if (sglq_gemm_run(g0, &g1, ws + o_aop1, (const int *)(ws + o_rexp1), P, Mpad, maxblk,
+      if (sglq_gemm_run(g0, &g1, ws + o_aop1, (const int *)(ws + o_rexp1), P, Mpad, gblk,
                         split1, nullptr, gu, mi, nullptr, st) != 0)
         return -1;
       // the down operands silu(g) * u (f32) as one f16 piece under the row's power of two (a
@@ -299,7 +306,7 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
       if (sglq_prep_a(d0, 0, gu, SGLQ_DT_F32, mi, P, Mpad, nullptr, 0, dsplit, ws + o_aop2,
                       (int *)(ws + o_rexp2), st, rowmax) != 0)
         return -1;
-      if (sglq_gemm_run(d0, &g2, ws + o_aop2, (const int *)(ws + o_rexp2), P, Mpad, maxblk,
+      if (sglq_gemm_run(d0, &g2, ws + o_aop2, (const int *)(ws + o_rexp2), P, Mpad, gblk,
                         dsplit, nullptr, o, E, nullptr, st) != 0)
         return -1;
     } else {
@@ -307,13 +314,13 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
       if (sglq_prep_a(g0, 1, h, h_dtype, E, P, Mpad, rowmap, 0, split1, ws + o_aop1,
                       (int *)(ws + o_rexp1), st) != 0)
         return -1;
-      if (sglq_gemm_run(g0, &g1, ws + o_aop1, (const int *)(ws + o_rexp1), P, Mpad, maxblk,
+      if (sglq_gemm_run(g0, &g1, ws + o_aop1, (const int *)(ws + o_rexp1), P, Mpad, gblk,
                         split1, nullptr, gu, 2 * mi, nullptr, st) != 0)
         return -1;
       if (sglq_prep_a(d0, 2, gu, SGLQ_DT_F32, 2 * mi, P, Mpad, nullptr, (int)mi, 1,
                       ws + o_aop2, (int *)(ws + o_rexp2), st) != 0)
         return -1;
-      if (sglq_gemm_run(d0, &g2, ws + o_aop2, (const int *)(ws + o_rexp2), P, Mpad, maxblk, 1,
+      if (sglq_gemm_run(d0, &g2, ws + o_aop2, (const int *)(ws + o_rexp2), P, Mpad, gblk, 1,
                         nullptr, o, E, nullptr, st) != 0)
         return -1;
     }

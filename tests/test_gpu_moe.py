@@ -35,7 +35,7 @@ def _experts(orc, n_exp, E, mi, seed, fmt="gptq4", std=0.02):
 
 
 def _check(orc, n_exp, E, mi, T, k, seed, dtypes=("bf16", "f32"), drop=False, fmt="gptq4",
-           std=0.02):
+           std=0.02, repeat=False):
     import torch
     import sgl_qlinear as q
     gu, dn, wgu, wdn = _experts(orc, n_exp, E, mi, seed, fmt, std)
@@ -44,6 +44,8 @@ def _check(orc, n_exp, E, mi, T, k, seed, dtypes=("bf16", "f32"), drop=False, fm
         ids[:] = -1
     elif drop:  # unrouted slots (id -1) are skipped
         ids[::3, -1] = -1
+    if repeat:  # every token lists token 0's first expert in its first two slots
+        ids[:, :2] = ids[0, 0]
     h = synth.normal(seed + 1000, (T, E))
     for dt in dtypes:
         if dt == "bf16":
@@ -130,3 +132,32 @@ def test_moe_decode_one_token_u8_g64(orc):
     _check(orc, 8, 512, 256, 1, 4, seed=99, fmt="gptq8_g64")
     _check(orc, 8, 512, 256, 1, 4, seed=100, fmt="gptq8_g64", dtypes=("f32",), drop=True)
 
+
+
+@pytest.mark.parametrize("T", [2, 4])
+@pytest.mark.parametrize("fmt", ["gptq4", "mxfp4", "gptq8"])
+def test_moe_decode_tokens(orc, T, fmt):
+    """2 and 4 tokens: routing launch, grouped wave-staged GEMVs over the experts' row blocks
+    (at most T rows each), then the combine; with and without unrouted slots, and with none
+    routed at all."""
+    _check(orc, 8, 512, 256, T, 3, seed=101 + T, fmt=fmt)
+    _check(orc, 6, 256, 384, T, 4, seed=111 + T, fmt=fmt, dtypes=("f32",), drop=True)
+    _check(orc, 4, 256, 128, T, 2, seed=121 + T, fmt=fmt, dtypes=("bf16",), drop="all")
+
+
+@pytest.mark.parametrize("T", [1, 2, 4])
+def test_moe_decode_repeated_experts(orc, T):
+    """Tokens that list one expert twice (and share it): that expert has more pairs than
+    there are tokens, so the routing cuts its rows into blocks of at most T rows, the rows the
+    decode GEMVs stage.  (One token takes slot-per-segment launches where its weights allow.)"""
+    _check(orc, 8, 256, 128, T, 3, seed=131 + T, repeat=True)
+
+
+def test_moe_decode_deepseek_shape_four_tokens(orc):
+    """BASELINE config 5, decode of four tokens (the bench's T = 4 line)."""
+    _check(orc, 64, 2048, 1408, 4, 6, seed=0x5EED0006, dtypes=("bf16",))
+
+
+def test_moe_decode_many_pairs(orc):
+    """Four tokens of 20 slots (80 pairs: more row blocks than experts)."""
+    _check(orc, 32, 256, 128, 4, 20, seed=141, dtypes=("f32",))
