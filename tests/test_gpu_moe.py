@@ -161,3 +161,17 @@ def test_moe_decode_deepseek_shape_four_tokens(orc):
 def test_moe_decode_many_pairs(orc):
     """Four tokens of 20 slots (80 pairs: more row blocks than experts)."""
     _check(orc, 32, 256, 128, 4, 20, seed=141, dtypes=("f32",))
+
+
+@pytest.mark.parametrize("fmt", ["gptq4", "mxfp4"])
+def test_moe_decode_one_token_repeated_experts(orc, fmt):
+    """One token listing an expert twice on the launches that take segments straight from the
+    routing (GPTQ4: the one-row kernel with the in-workgroup combine; MXFP4: the wave-staged
+    kernel with the fused combine): each slot stays its own segment."""
+    _check(orc, 8, 512, 256, 1, 3, seed=151, fmt=fmt, repeat=True)
+
+
+def test_moe_prefill_repeated_experts(orc):
+    """Prefill rows where every token lists one shared expert twice: that expert's 80 rows
+    span two 64-row blocks."""
+    _check(orc, 8, 256, 128, 40, 3, seed=161, repeat=True)
