@@ -3,7 +3,7 @@
 those alone give 200 tiles), against the reference CPU path (oracle dequant +
 sgl_matmul_nt).  Covers 8-bit codes, MXFP4, f32 rows (two A pieces), ragged M and N, K that
 is not a whole number of four-chunk loop bodies (chunks past the end computed with zero
-scales), bias, and the 8-wave tile.  Tolerance (BASELINE): max|y - y_ref| / max|y_ref| <= 1e-3."""
+scales), bias, the 8-wave tile, and at most 64 rows (64-row tiles, K split over workgroups).  Tolerance (BASELINE): max|y - y_ref| / max|y_ref| <= 1e-3."""
 import numpy as np
 import pytest
 
@@ -20,6 +20,10 @@ CASES = [
     ("mxfp4", 9616, 1024, 520, "bf16", True),    # e2m1 with block and column exponents
     ("gptq4", 7696, 2048, 300, "f32", True),     # f32 rows: hi + lo pieces on 64-row tiles
     ("awq4", 8000, 1024, 2000, "bf16", False),   # 16 x 21 tiles of 384 columns: 8 waves
+    # at most 64 rows: 64-row tiles, K split over workgroups, k_splitk_reduce adds the slices
+    ("gptq4", 4000, 4096, 40, "bf16", True),     # 21 column blocks (ragged), K in 8 slices
+    ("gptq4", 4000, 2048, 64, "f32", True),      # f32 rows on the 64-row tile
+    ("mxfp4", 3000, 1408, 33, "bf16", True),     # 11 chunks over the slices, e2m1
 ]
 
 
