@@ -175,3 +175,21 @@ def test_moe_prefill_repeated_experts(orc):
     """Prefill rows where every token lists one shared expert twice: that expert's 80 rows
     span two 64-row blocks."""
     _check(orc, 8, 256, 128, 40, 3, seed=161, repeat=True)
+
+
+@pytest.mark.parametrize("T", [1, 3, 9])
+def test_moe_single_expert(orc, T):
+    """One expert, one slot per token: decode and prefill launches with a single segment."""
+    _check(orc, 1, 256, 128, T, 1, seed=171 + T, dtypes=("f32",))
+
+
+@pytest.mark.parametrize("T", [1, 4, 40])
+def test_moe_one_intermediate_tile(orc, T):
+    """An intermediate size of one 16-column tile (gate/up of two tiles, down K of 16)."""
+    _check(orc, 4, 128, 16, T, 2, seed=181 + T, dtypes=("bf16",))
+
+
+def test_moe_every_expert(orc):
+    """Every token routed to every expert (k = n_exp): every segment holds every token."""
+    _check(orc, 6, 256, 128, 2, 6, seed=191)
+    _check(orc, 6, 256, 128, 20, 6, seed=192, dtypes=("f32",))
