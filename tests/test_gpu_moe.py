@@ -51,6 +51,9 @@ def _check(orc, n_exp, E, mi, T, k, seed, dtypes=("bf16", "f32"), drop=False, fm
         if dt == "bf16":
             hb = synth.bf16_bits_to_f32(synth.to_bf16_bits(h))
             th = torch.from_numpy(hb).cuda().to(torch.bfloat16)
+        elif dt == "f16":
+            hb = h.astype(np.float16).astype(np.float32)
+            th = torch.from_numpy(hb).cuda().to(torch.float16)
         else:
             hb, th = h, torch.from_numpy(h).cuda()
         print(f"[gpu] moe {fmt} n_exp={n_exp} E={E} mi={mi} T={T} k={k} {dt}", flush=True)
@@ -193,3 +196,10 @@ def test_moe_every_expert(orc):
     """Every token routed to every expert (k = n_exp): every segment holds every token."""
     _check(orc, 6, 256, 128, 2, 6, seed=191)
     _check(orc, 6, 256, 128, 20, 6, seed=192, dtypes=("f32",))
+
+
+@pytest.mark.parametrize("T", [1, 3, 40])
+@pytest.mark.parametrize("fmt", ["gptq4", "mxfp4"])
+def test_moe_f16_tokens(orc, T, fmt):
+    """f16 token rows: one token (slot-per-segment launches), a decode batch, and prefill."""
+    _check(orc, 8, 512, 256, T, 3, seed=201 + T, fmt=fmt, dtypes=("f16",))
