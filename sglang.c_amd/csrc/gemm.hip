@@ -1558,7 +1558,6 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
 
 template <int KIND, int NP, int BN, int SSX, int WMW, int NBUF, int MB = 4, int RS = 1>
 void launch_lds1(const GemmArgs &a, dim3 grid, hipStream_t st) {
-  static bool raised = false;
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
   constexpr int SS = SSX < SPC ? SSX : SPC;
   // LDS: NBUF x (A: NP pieces x SS steps x 4 x rows, B: BN/16 tiles x SS steps x 64) x 16 B
@@ -1570,9 +1569,8 @@ void launch_lds1(const GemmArgs &a, dim3 grid, hipStream_t st) {
     launch_lds1<KIND, NP, BN, 2, WMW, 2, MB, RS>(a, grid, st);
   } else {
     auto f = k_gemm_lds<KIND, NP, BN, SSX, WMW, NBUF, MB, RS>;
-    if (!raised)
-      raised = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   160 * 1024) == hipSuccess;
+    static unsigned long long raised = 0;
+    sglq_raise_lds((const void *)f, 160 * 1024, &raised);
     f<<<grid, 128 * WMW, lds, st>>>(a);
   }
 }
@@ -1596,11 +1594,9 @@ void launch_breg1(const GemmArgs &a, dim3 grid, hipStream_t st) {
   constexpr int D = 2;
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
   constexpr size_t lds = (size_t)2 * NP * SPC * 4 * 64 * 16;
-  static bool raised = false;
+  static unsigned long long raised = 0;
   auto f = k_gemm_breg<KIND, NP, WN, TN, D>;
-  if (!raised)
-    raised = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 160 * 1024) == hipSuccess;
+  sglq_raise_lds((const void *)f, 160 * 1024, &raised);
   f<<<grid, 64 * WN, lds, st>>>(a);
 }
 // Wave layout of the grouped launches, from a sweep at the DeepSeek shapes (64 experts, 48
@@ -1658,18 +1654,14 @@ void launch_dma(const GemmArgs &a, int mb, int wn, dim3 grid, hipStream_t st) {
 template <int KIND, bool SPLIT, bool SCF16, bool STEPM, bool PS, int MB>
 void launch_bn(const GemmArgs &a, int bn, unsigned grid, size_t lds, hipStream_t st) {
   // LDS beyond 64 KiB must be enabled per kernel once (160 KiB on gfx950)
-  static bool raised128 = false, raised64 = false;
+  static unsigned long long raised128 = 0, raised64 = 0;
   if (bn == 128) {
     auto f = k_gemm<KIND, SPLIT, SCF16, STEPM, 128, PS, MB>;
-    if (!raised128)
-      raised128 = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      160 * 1024) == hipSuccess;
+    sglq_raise_lds((const void *)f, 160 * 1024, &raised128);
     f<<<grid, 256, lds, st>>>(a);
   } else {
     auto f = k_gemm<KIND, SPLIT, SCF16, STEPM, 64, PS, MB>;
-    if (!raised64)
-      raised64 = hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     160 * 1024) == hipSuccess;
+    sglq_raise_lds((const void *)f, 160 * 1024, &raised64);
     f<<<grid, 256, lds, st>>>(a);
   }
 }

@@ -500,13 +500,17 @@ bool launch_row_grp2(const RowArgs &a, int cpw, dim3 grid, size_t lds, hipStream
 template <int KIND, int C, bool MV>
 void launch_row_grp3c(const RowArgs &a, dim3 grid, size_t lds, hipStream_t st) {
   auto f = k_gemv_row<KIND, C, 1, SGLQ_DT_F32, true, MV, 16, 3>;
-  // dynamic LDS beyond 64 KiB is enabled per kernel; the request must leave room for the
-  // kernel's static LDS (the slice sums) within the 160 KiB of a workgroup
-  static size_t raised = 0;
-  if (lds > 64 * 1024 && lds > raised &&
+  // dynamic LDS beyond 64 KiB is enabled per kernel and device; the request must leave room
+  // for the kernel's static LDS (the slice sums) within the 160 KiB of a workgroup, so it is
+  // exactly this launch's size, raised again when a larger one comes
+  static size_t raised[64];
+  int dev = 0;
+  if (lds > 64 * 1024 && hipGetDevice(&dev) == hipSuccess &&
+      (dev >= 64 || lds > raised[dev]) &&
       hipFuncSetAttribute((const void *)f, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)lds) == hipSuccess)
-    raised = lds;
+                          (int)lds) == hipSuccess &&
+      dev < 64)
+    raised[dev] = lds;
   f<<<grid, 1024, lds, st>>>(a);
 }
 template <int KIND>

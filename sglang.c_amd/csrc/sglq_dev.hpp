@@ -93,6 +93,20 @@ static inline unsigned sglq_blocks(int64_t n, int threads) {
   return (unsigned)((n + threads - 1) / threads);
 }
 
+// Dynamic LDS beyond 64 KiB is enabled per kernel and per device: raises kernel f's limit to
+// `bytes` on the current device once (*done keeps one bit per device; devices past 63 are
+// raised on every call).  Returns false when the runtime refuses.
+inline bool sglq_raise_lds(const void *f, int bytes, unsigned long long *done) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  const unsigned long long bit = dev < 64 ? 1ull << dev : 0;
+  if (bit && (__atomic_load_n(done, __ATOMIC_ACQUIRE) & bit)) return true;
+  if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
+    return false;
+  if (bit) __atomic_fetch_or(done, bit, __ATOMIC_ACQ_REL);
+  return true;
+}
+
 // Grow d->ws / d->aux to at least `bytes` (device memory; an outgrown buffer stays allocated
 // until the handle is freed, since a graph captured earlier may hold its address).
 int sglq_aux_reserve(sglq_dev *d, size_t bytes);
