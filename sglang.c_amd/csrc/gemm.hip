@@ -995,8 +995,9 @@ __device__ void swiglu_epilogue(const GemmArgs &a, const float4_t (&acc)[MBW][TN
 // the scaled fp4 conversion), so the products are bit-identical to k_gemm_lds.  Only the A
 // operands (64 rows, one chunk per stage) go through a double-buffered LDS ring, one chunk
 // ahead in registers.  blockIdx.y selects a slice of the chunks when the call is split over K.
-template <int KIND, int NP, int WN, int TN, int D>
-__global__ __launch_bounds__(64 * WN, 2) void k_gemm_breg(GemmArgs a) {
+// MINB: waves per SIMD the register budget must allow.
+template <int KIND, int NP, int WN, int TN, int D, int MINB = 2>
+__global__ __launch_bounds__(64 * WN, MINB) void k_gemm_breg(GemmArgs a) {
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
   constexpr int MB = 4, BMR = 64, NT16 = WN * TN, NTH = 64 * WN;
   constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
@@ -1101,11 +1102,13 @@ __global__ __launch_bounds__(64 * WN, 2) void k_gemm_breg(GemmArgs a) {
     }
 #pragma unroll
     for (int s = 0; s < SPC; s++) {
-      half8_t bv[TN], av[NP][MB];
+      half8_t av[NP][MB];
 #pragma unroll
       for (int p = 0; p < NP; p++)
 #pragma unroll
         for (int i = 0; i < MB; i++) av[p][i] = sa[((p * SPC + s) * 4 + kq) * BMR + i * 16];
+      // each unpacked weight fragment feeds its MB (x NP) MFMAs at once, so one fragment is
+      // live at a time (fewer registers: three workgroups per CU)
 #pragma unroll
       for (int j = 0; j < TN; j++) {
         const float fsc = E2M1 ? e8m0_rel((cm[j] >> (8 * s)) & 255u, cref[j]) : 1.f;
@@ -1115,24 +1118,21 @@ __global__ __launch_bounds__(64 * WN, 2) void k_gemm_breg(GemmArgs a) {
 #pragma unroll
           for (int hh = 0; hh < 4; hh++) u.h[hh] = u.h[hh] * s2[j];
         }
-        bv[j] = u.v;
+#pragma unroll
+        for (int p = 0; p < NP; p++)
+#pragma unroll
+          for (int i = 0; i < MB; i++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[p][i], u.v, acc[i][j], 0, 0, 0);
       }
-#pragma unroll
-      for (int p = 0; p < NP; p++)
-#pragma unroll
-        for (int i = 0; i < MB; i++)
-#pragma unroll
-          for (int j = 0; j < TN; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[p][i], bv[j], acc[i][j], 0, 0, 0);
     }
   };
 
   // Chunk k of the slice: its codes were loaded D chunks earlier into ring slot k % D (the
   // loop is unrolled by D so every slot is named at compile time); its A operands sit in LDS
-  // buffer k & 1.  An iteration takes chunk k's codes out of the ring, refills the slot with
-  // chunk k + D, multiplies, then writes chunk k + 1's A operands (loaded one iteration
-  // earlier) into the other buffer and loads chunk k + 2's.  Loads past the slice reload its
-  // last chunk (valid memory, never used).
+  // buffer k & 1.  An iteration multiplies chunk k from its ring slot, refills the slot with
+  // chunk k + D, then writes chunk k + 1's A operands (loaded one iteration earlier) into the
+  // other buffer and loads chunk k + 2's.  Loads past the slice reload its last chunk (valid
+  // memory, never used).
   u32x4_t bq[D][TN];
   uint32_t mq[D][TN];
   half8_t ar[AIPT];
@@ -1148,15 +1148,11 @@ __global__ __launch_bounds__(64 * WN, 2) void k_gemm_breg(GemmArgs a) {
     for (int u = 0; u < D; u++) {
       const int k = kb + u;
       if (k < nc) {
-        u32x4_t cw[TN];
-        uint32_t cm[TN];
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-          cw[j] = bq[u][j];
-          cm[j] = mq[u][j];
-        }
+        // multiply from the ring slot, then refill it: D sets of codes live, not D + 1
+        // (copying a slot out before its refill cost the registers of a third workgroup per
+        // CU; config 5 prefill 176 -> 163-170 us with the third)
+        compute(k & 1, bq[u], mq[u]);
         load_b(min(c0 + k + D, c1 - 1), bq[u], mq[u]);
-        compute(k & 1, cw, cm);
         store_a((k + 1) & 1, ar);
         load_a(min(c0 + k + 2, c1 - 1), ar);
         __syncthreads();
@@ -1589,13 +1585,13 @@ int lds_cols(int cfg) { return cfg == LDS_128x64 ? 64 : 128; }
 // us for k_gemm_lds; the wave layouts below improve on that.  Dense calls of at most 64 rows
 // stay on k_gemm_lds (21.7 vs 22.6 us at M = 64 on [11008, 4096], where the split over K
 // leaves each workgroup only 5 chunks).
-template <int KIND, int NP, int WN, int TN>
+template <int KIND, int NP, int WN, int TN, int MINB = 2>
 void launch_breg1(const GemmArgs &a, dim3 grid, hipStream_t st) {
   constexpr int D = 2;
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
   constexpr size_t lds = (size_t)2 * NP * SPC * 4 * 64 * 16;
   static unsigned long long raised = 0;
-  auto f = k_gemm_breg<KIND, NP, WN, TN, D>;
+  auto f = k_gemm_breg<KIND, NP, WN, TN, D, MINB>;
   sglq_raise_lds((const void *)f, 160 * 1024, &raised);
   f<<<grid, 64 * WN, lds, st>>>(a);
 }
@@ -1610,8 +1606,10 @@ static void breg_shape(int np, int &wn, int &tn) {
 }
 template <int KIND, int NP>
 void launch_breg(const GemmArgs &a, dim3 grid, hipStream_t st) {
+  // one piece of int codes: three waves per SIMD (three workgroups per CU: 168 registers, the
+  // grid's row blocks in about one round).  MXFP4 codes keep two (three would spill).
   if constexpr (NP == 1)
-    launch_breg1<KIND, NP, 4, 4>(a, grid, st);
+    launch_breg1<KIND, NP, 4, 4, KIND != SGLQ_KIND_E2M1 ? 3 : 2>(a, grid, st);
   else
     launch_breg1<KIND, NP, 8, 2>(a, grid, st);
 }
