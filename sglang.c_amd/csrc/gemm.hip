@@ -1835,7 +1835,11 @@ static WidePlan wide_plan(const sglq_dev *d, int64_t M, int np) {
     return p;
   }
   const int64_t bmr = 16 * p.mb, nbm = (M + bmr - 1) / bmr;
-  if (nbm * ((d->N + 383) / 384) >= 200) {
+  // MXFP4 codes spill in the 8-wave tile (256 registers): it pays only from about twice as
+  // many tiles ([8192, 4096] bf16: M = 2048 284.3 -> 254.8 us on 4 waves, M = 4096 452.6 us
+  // on 8 against 477.0 on 4)
+  const int64_t min8 = d->kind == SGLQ_KIND_E2M1 ? 400 : 200;
+  if (nbm * ((d->N + 383) / 384) >= min8) {
     p.use = 1;
     p.wn = 8;
   } else if (nbm * ((d->N + 191) / 192) >= 200) {

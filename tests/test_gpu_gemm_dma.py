@@ -24,6 +24,7 @@ CASES = [
     ("gptq4", 4000, 4096, 40, "bf16", True),     # 21 column blocks (ragged), K in 8 slices
     ("gptq4", 4000, 2048, 64, "f32", True),      # f32 rows on the 64-row tile
     ("mxfp4", 3000, 1408, 33, "bf16", True),     # 11 chunks over the slices, e2m1
+    ("mxfp4", 7700, 1024, 4100, "bf16", True),   # 33 x 21 tiles of 384 columns: 8 waves, e2m1
 ]
 
 
