@@ -1336,8 +1336,8 @@ __device__ __forceinline__ bool wide_tile(const GemmArgs &a, int &bm, int &bn) {
 //     SIMD) the A fragments of a chunk are read up front and the unpack of step s + 1 is
 //     interleaved with step s's MFMAs (SCHED); 8 waves (two per SIMD) overlap each other.
 // Products are those of k_gemm_lds (same prescale and unpack); the epilogue stores whole rows.
-template <int KIND, int NP, int TN, int MB, bool SCHED, int WN>
-__global__ __launch_bounds__(64 * WN, 1) void k_gemm_dma(GemmArgs a) {
+template <int KIND, int NP, int TN, int MB, bool SCHED, int WN, int MINB = 1>
+__global__ __launch_bounds__(64 * WN, MINB) void k_gemm_dma(GemmArgs a) {
   constexpr int SPC = KIND == SGLQ_KIND_U8 ? 2 : 4;
   constexpr bool E2M1 = KIND == SGLQ_KIND_E2M1;
   constexpr int BMR = 16 * MB;
@@ -1633,9 +1633,11 @@ void launch_dma1(const GemmArgs &a, dim3 grid, hipStream_t st) {
 // shapes of k_gemm_dma: 128 rows x 192 columns (4 waves) or x 384 columns (8 waves); two A
 // pieces (f32 rows) use 64-row tiles, the largest whose four A buffers fit the LDS
 template <int KIND, int NP>
-void launch_dma(const GemmArgs &a, int mb, int wn, dim3 grid, hipStream_t st) {
+void launch_dma(const GemmArgs &a, int mb, int wn, bool occ2, dim3 grid, hipStream_t st) {
   if constexpr (NP == 1) {
-    if (mb == 4)  // up to 64 rows
+    if (mb == 4 && occ2)  // 64-row tiles beyond 64 rows, two workgroups per CU
+      k_gemm_dma<KIND, NP, 3, 4, false, 4, 2><<<grid, 256, 0, st>>>(a);
+    else if (mb == 4)  // up to 64 rows
       launch_dma1<KIND, NP, 3, 4, 4>(a, grid, st);
     else if (wn == 8)
       launch_dma1<KIND, NP, 3, 8, 8>(a, grid, st);
@@ -1811,9 +1813,10 @@ static LdsPlan lds_plan(const sglq_dev *d, int64_t M) {
 // SGLQ_GEMM_DMA=0 keeps every call on k_gemm_lds (A/B measurement).
 struct WidePlan {
   int use, mb, wn, nz;  // wn waves along N, nz slices of K (partials added by k_splitk_reduce)
+  int occ2;             // 64-row tiles of more than 64 rows: two waves per SIMD (see below)
 };
 static WidePlan wide_plan(const sglq_dev *d, int64_t M, int np) {
-  WidePlan p = {0, np == 1 ? 8 : 4, 4, 1};
+  WidePlan p = {0, np == 1 ? 8 : 4, 4, 1, 0};
   static int env = -1, small = -1;
   if (env < 0) {
     const char *e = getenv("SGLQ_GEMM_DMA");
@@ -1844,6 +1847,16 @@ static WidePlan wide_plan(const sglq_dev *d, int64_t M, int np) {
     p.wn = 8;
   } else if (nbm * ((d->N + 191) / 192) >= 200) {
     p.use = 1;
+  } else if (np == 1 && ((M + 63) / 64) * ((d->N + 191) / 192) >= 170) {
+    // too few 128-row tiles but enough 64-row ones: 64 x 192 tiles with the A fragments read
+    // per step (186 registers), so two workgroups share a CU and one wave's unpack runs
+    // beside the other's MFMAs.  [11008, 4096] bf16 against k_gemm_lds: M = 160 69.1 -> 58.0
+    // us, 256 69.3 -> 60.4, 320 87.3 -> 80.6, 384 88.4 -> 83.0.  With fewer tiles it measured
+    // slower (M = 128: 47.7 -> 56.4; [4096, 4096] M = 256: 39.8 -> 55.4), as it did in place
+    // of the 128-row tiles (M = 512: 83.8 -> 89.5).
+    p.use = 1;
+    p.mb = 4;
+    p.occ2 = 1;
   }
   return p;
 }
@@ -1923,16 +1936,16 @@ int sglq_gemm_run(const sglq_dev *d, const sglq_group *grp, const void *aop,
       const dim3 grid2((unsigned)(8 * ((a.nbm * a.nbn + 7) / 8)), (unsigned)wp.nz);
       switch (d->kind) {
         case SGLQ_KIND_U4:
-          if (split) launch_dma<SGLQ_KIND_U4, 2>(a, wp.mb, wp.wn, grid2, st);
-          else launch_dma<SGLQ_KIND_U4, 1>(a, wp.mb, wp.wn, grid2, st);
+          if (split) launch_dma<SGLQ_KIND_U4, 2>(a, wp.mb, wp.wn, wp.occ2, grid2, st);
+          else launch_dma<SGLQ_KIND_U4, 1>(a, wp.mb, wp.wn, wp.occ2, grid2, st);
           break;
         case SGLQ_KIND_U8:
-          if (split) launch_dma<SGLQ_KIND_U8, 2>(a, wp.mb, wp.wn, grid2, st);
-          else launch_dma<SGLQ_KIND_U8, 1>(a, wp.mb, wp.wn, grid2, st);
+          if (split) launch_dma<SGLQ_KIND_U8, 2>(a, wp.mb, wp.wn, wp.occ2, grid2, st);
+          else launch_dma<SGLQ_KIND_U8, 1>(a, wp.mb, wp.wn, wp.occ2, grid2, st);
           break;
         default:
-          if (split) launch_dma<SGLQ_KIND_E2M1, 2>(a, wp.mb, wp.wn, grid2, st);
-          else launch_dma<SGLQ_KIND_E2M1, 1>(a, wp.mb, wp.wn, grid2, st);
+          if (split) launch_dma<SGLQ_KIND_E2M1, 2>(a, wp.mb, wp.wn, wp.occ2, grid2, st);
+          else launch_dma<SGLQ_KIND_E2M1, 1>(a, wp.mb, wp.wn, wp.occ2, grid2, st);
           break;
       }
       SGLQ_HIP(hipGetLastError());

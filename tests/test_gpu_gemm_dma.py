@@ -3,7 +3,8 @@
 those alone give 200 tiles), against the reference CPU path (oracle dequant +
 sgl_matmul_nt).  Covers 8-bit codes, MXFP4, f32 rows (two A pieces), ragged M and N, K that
 is not a whole number of four-chunk loop bodies (chunks past the end computed with zero
-scales), bias, the 8-wave tile, and at most 64 rows (64-row tiles, K split over workgroups).  Tolerance (BASELINE): max|y - y_ref| / max|y_ref| <= 1e-3."""
+scales), bias, the 8-wave tile, at most 64 rows (64-row tiles, K split over workgroups), and
+the 64-row tiles that run two workgroups per CU where 128-row tiles are too few.  Tolerance (BASELINE): max|y - y_ref| / max|y_ref| <= 1e-3."""
 import numpy as np
 import pytest
 
@@ -25,6 +26,10 @@ CASES = [
     ("gptq4", 4000, 2048, 64, "f32", True),      # f32 rows on the 64-row tile
     ("mxfp4", 3000, 1408, 33, "bf16", True),     # 11 chunks over the slices, e2m1
     ("mxfp4", 7700, 1024, 4100, "bf16", True),   # 33 x 21 tiles of 384 columns: 8 waves, e2m1
+    # too few 128-row tiles, enough 64-row ones: 64 x 192 tiles, two workgroups per CU
+    ("gptq4", 7000, 2048, 300, "bf16", True),    # 5 x 37 tiles, ragged M and N
+    ("gptq8", 6000, 1024, 350, "bf16", False),   # 8-bit codes
+    ("mxfp4", 9000, 1408, 250, "bf16", True),    # e2m1, 11 chunks
 ]
 
 
