@@ -165,8 +165,8 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
     const int64_t E = g0->K, mi = d0->K, P = T * k;
     // row blocks: at most 64 rows of one expert for the grouped GEMMs (at most gblk blocks,
     // the GEMMs' grid); at most T rows for the decode GEMVs, whose staging holds T rows (a token
-    // that lists an expert twice gives it more rows than there are tokens), so there at most
-    // one block per pair.  maxblk = the table's capacity.
+    // that lists an expert twice gives it more rows than there are tokens), at most one block
+    // per pair.  maxblk = the table's capacity.
     const int64_t gblk = (P + SGLQ_MOE_BM - 1) / SGLQ_MOE_BM + n_exp;
     const int64_t maxblk = std::max<int64_t>(gblk, P);
     const int64_t Mpad = (P + SGLQ_GEMM_BM - 1) / SGLQ_GEMM_BM * SGLQ_GEMM_BM + SGLQ_GEMM_BM;
