@@ -1334,7 +1334,8 @@ __device__ __forceinline__ bool wide_tile(const GemmArgs &a, int &bm, int &bn) {
 //   * VALU work does not issue in the shadow of the same wave's MFMAs on gfx950 (measured with
 //     k_mfma_valu), so the unpack is kept to one pass per workgroup, and with 4 waves (one per
 //     SIMD) the A fragments of a chunk are read up front and the unpack of step s + 1 is
-//     interleaved with step s's MFMAs (SCHED); 8 waves (two per SIMD) overlap each other.
+//     interleaved with step s's MFMAs (SCHED); 8 waves (two per SIMD) overlap each other, and
+//     so do two workgroups of 64-row tiles (MINB = 2 waves per SIMD, A fragments per step).
 // Products are those of k_gemm_lds (same prescale and unpack); the epilogue stores whole rows.
 template <int KIND, int NP, int TN, int MB, bool SCHED, int WN, int MINB = 1>
 __global__ __launch_bounds__(64 * WN, MINB) void k_gemm_dma(GemmArgs a) {
@@ -1582,9 +1583,9 @@ int lds_cols(int cfg) { return cfg == LDS_128x64 ? 64 : 128; }
 // k_gemm_breg for the grouped (MoE) launches, codes 2 chunks ahead (3-4 chunks measured 2-8%
 // slower).  On k_gemm_lds's 64 x 128 tile it measured 105.7 us (gate/up with the SwiGLU
 // epilogue) and 69.9 us (down, f32 operands) at the DeepSeek shapes, against 123.2 and 114.3
-// us for k_gemm_lds; the wave layouts below improve on that.  Dense calls of at most 64 rows
-// stay on k_gemm_lds (21.7 vs 22.6 us at M = 64 on [11008, 4096], where the split over K
-// leaves each workgroup only 5 chunks).
+// us for k_gemm_lds; the wave layouts below improve on that.  (Dense calls of at most 64 rows
+// measured 21.7 us on k_gemm_lds against 22.6 on this kernel at M = 64, [11008, 4096]; they
+// now take k_gemm_dma.)
 template <int KIND, int NP, int WN, int TN, int MINB = 2>
 void launch_breg1(const GemmArgs &a, dim3 grid, hipStream_t st) {
   constexpr int D = 2;
