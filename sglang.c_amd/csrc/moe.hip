@@ -296,13 +296,16 @@ extern "C" int sglq_moe_forward(sglq_dev *const *gate_up, sglq_dev *const *down,
       // the down operands silu(g) * u (f32) as one f16 piece under the row's power of two (a
       // 2^-12 relative rounding, as the prescaled weights'): half the MFMAs and operand bytes
       // of the hi + lo split.  Config 5 prefill 199 -> 174 us; max rel error against the
-      // reference 3.2e-4 -> 3.9e-4 (at most 5.2e-4 over the MoE tests; bar 1e-3).
-      // SGLQ_MOE_DOWN_SPLIT=1 keeps hi + lo.
-      static int dsplit = -1;
-      if (dsplit < 0) {
+      // reference 3.2e-4 -> 3.9e-4 (at most 5.2e-4 over the MoE tests; bar 1e-3).  Below 256
+      // intermediate columns the down products are too few for that rounding to average out
+      // (mi = 16, 8-bit experts: 1.06e-3 on one piece, 7.0e-4 on hi + lo), so they keep hi + lo.
+      // SGLQ_MOE_DOWN_SPLIT=1 / 0 forces either.
+      static int dsplit_env = -2;
+      if (dsplit_env == -2) {
         const char *e = getenv("SGLQ_MOE_DOWN_SPLIT");
-        dsplit = e ? atoi(e) : 0;
+        dsplit_env = e ? atoi(e) : -1;
       }
+      const int dsplit = dsplit_env >= 0 ? dsplit_env : mi < 256 ? 1 : 0;
       if (sglq_prep_a(d0, 0, gu, SGLQ_DT_F32, mi, P, Mpad, nullptr, 0, dsplit, ws + o_aop2,
                       (int *)(ws + o_rexp2), st, rowmax) != 0)
         return -1;

@@ -203,3 +203,10 @@ def test_moe_every_expert(orc):
 def test_moe_f16_tokens(orc, T, fmt):
     """f16 token rows: one token (slot-per-segment launches), a decode batch, and prefill."""
     _check(orc, 8, 512, 256, T, 3, seed=201 + T, fmt=fmt, dtypes=("f16",))
+
+
+def test_moe_prefill_short_intermediate(orc):
+    """An intermediate size of one tile (16) with 8-bit experts: the down products are too few
+    to average the rounding of one-piece f16 operands (1.06e-3 on one piece), so below 256
+    intermediate columns the down operands keep hi + lo pieces.  Found by a randomized sweep."""
+    _check(orc, 17, 384, 16, 64, 4, seed=499866, fmt="gptq8", dtypes=("bf16",), repeat=True)
