@@ -59,6 +59,12 @@ __global__ __launch_bounds__(256) void k_router_logits(const float *__restrict__
   }
 }
 
+// e^x rounded once to float from a double-precision exp: the correctly rounded value except
+// within about 2^-29 of a rounding midpoint.  The reference's host expf (glibc) is correctly
+// rounded for all but a sliver of inputs, so the scores, and the experts chosen at near-ties,
+// match it far more often than a single-precision device expf (1 ulp) does.
+__device__ __forceinline__ float expf_cr(float x) { return (float)exp((double)x); }
+
 __global__ __launch_bounds__(64) void k_moe_gate(const float *__restrict__ logits, int ne,
                                                  const float *__restrict__ bias, int sigmoid,
                                                  int ng, int tg, int k, int norm, float scale,
@@ -77,7 +83,7 @@ __global__ __launch_bounds__(64) void k_moe_gate(const float *__restrict__ logit
   }
   if (sigmoid) {
 #pragma unroll
-    for (int q = 0; q < 4; q++) v[q] = 1.0f / (1.0f + expf(-v[q]));
+    for (int q = 0; q < 4; q++) v[q] = 1.0f / (1.0f + expf_cr(-v[q]));
   } else {
     // softmax as reference src/ops.c:220-231: max, expf(x - max), double sum in index order,
     // one float reciprocal
@@ -88,7 +94,7 @@ __global__ __launch_bounds__(64) void k_moe_gate(const float *__restrict__ logit
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      v[q] = expf(v[q] - mx);
+      v[q] = expf_cr(v[q] - mx);
       if (lane + 64 * q < ne) s_s[lane + 64 * q] = v[q];
     }
     __syncthreads();
