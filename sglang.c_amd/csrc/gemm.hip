@@ -1150,7 +1150,7 @@ __global__ __launch_bounds__(64 * WN, MINB) void k_gemm_breg(GemmArgs a) {
       if (k < nc) {
         // multiply from the ring slot, then refill it: D sets of codes live, not D + 1
         // (copying a slot out before its refill cost the registers of a third workgroup per
-        // CU; config 5 prefill 176 -> 163-170 us with the third)
+        // CU; config 5 prefill 174-177 -> 163-174 us with the third)
         compute(k & 1, bq[u], mq[u]);
         load_b(min(c0 + k + D, c1 - 1), bq[u], mq[u]);
         store_a((k + 1) & 1, ar);
